@@ -1,0 +1,95 @@
+"""The C-ABI library (CPU only, no kernel launches): it loads, exports every symbol that
+include/tattn.h declares, agrees with the header's constants, describes its tile tables, and
+rejects bad arguments with error codes and messages before touching a device."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from tattn import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "tattn.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(tattn_\w+)\s*\(", text, re.M)))
+
+
+def test_library_loads_with_matching_abi():
+    lib = _lib.load()
+    assert lib.tattn_abi_version() == _lib.ABI_VERSION
+    assert f"#define TATTN_ABI_VERSION {_lib.ABI_VERSION}" in HEADER.read_text()
+
+
+def test_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared()
+    assert names == sorted(_lib.EXPORTS)
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_header_constants_match_binding():
+    text = HEADER.read_text()
+    assert "TATTN_F16 = 0" in text and "TATTN_F32 = 1" in text
+    assert "TATTN_K_FWD = 0" in text and "TATTN_K_BWD_DKDV = 1" in text and "TATTN_K_BWD_DQ = 2" in text
+    assert ctypes.sizeof(_lib.TattnConfig) == 24
+
+
+@pytest.mark.parametrize("kernel", [_lib.K_FWD, _lib.K_BWD_DKDV, _lib.K_BWD_DQ])
+@pytest.mark.parametrize("d", [16, 32, 64, 128])
+@pytest.mark.parametrize("dtype", [_lib.F16, _lib.F32])
+def test_tables_are_described(kernel, d, dtype):
+    n = _lib.num_configs(kernel, d, dtype)
+    assert n >= 1
+    for c in range(n):
+        desc = _lib.config_desc(kernel, d, dtype, c)
+        assert desc["waves"] in (4, 8) and desc["tiles"] in (1, 2)
+        rows = desc["waves"] * desc["tiles"] * 32
+        own = desc["block_n"] if kernel == _lib.K_BWD_DKDV else desc["block_m"]
+        assert own == rows
+        assert 0 < desc["lds_bytes"] <= 160 * 1024
+    with pytest.raises(RuntimeError, match="no config"):
+        _lib.config_desc(kernel, d, dtype, n)
+    assert 0 <= _lib.pick_config(kernel, d, dtype, False, 4096) < n
+
+
+def test_unsupported_head_dim_has_no_table():
+    assert _lib.num_configs(_lib.K_FWD, 48, _lib.F16) == -1
+
+
+def _fwd_args(**kw):
+    st = (ctypes.c_int64 * 4)(16 * 64, 64, 64, 1)
+    a = dict(q=16, k=16, v=16, o=16, m=16, qs=st, ks=st, vs=st, os=st, Z=1, H=1, N=16, D=64,
+             dtype=_lib.F16, causal=0, scale=0.125, cfg=-1, stream=None)
+    a.update(kw)
+    return [a[x] for x in ("q", "k", "v", "o", "m", "qs", "ks", "vs", "os", "Z", "H", "N", "D",
+                           "dtype", "causal", "scale", "cfg", "stream")]
+
+
+@pytest.mark.parametrize("bad,msg", [
+    (dict(D=48), "head dim"),
+    (dict(dtype=7), "dtype"),
+    (dict(N=0), "positive"),
+    (dict(q=None), "q is a null pointer"),
+    (dict(k=24), "16-byte aligned"),
+    (dict(qs=(ctypes.c_int64 * 4)(1024, 64, 64, 2)), "d stride"),
+    (dict(vs=(ctypes.c_int64 * 4)(1024, 64, 12, 1)), "multiple of"),
+    (dict(cfg=999), "out of range"),
+])
+def test_fwd_rejects_bad_arguments_before_launch(bad, msg):
+    lib = _lib.load()
+    rc = lib.tattn_fwd(*_fwd_args(**bad))
+    assert rc in (1, 2)
+    assert msg in _lib.last_error()
+
+
+def test_bwd_rejects_bad_config_for_both_tables():
+    lib = _lib.load()
+    st = (ctypes.c_int64 * 4)(1024, 64, 64, 1)
+    rc = lib.tattn_bwd(16, 16, 16, 16, 16, 16, 16, 16, 16, 16, st, 1, 1, 16, 64, _lib.F16, 0,
+                       0.125, 99, None)
+    assert rc == 2 and "out of range" in _lib.last_error()

@@ -1,0 +1,65 @@
+"""Host-side behaviour of the public API that needs no GPU: argument checks with the reference's
+messages (src/tattn/api.py:45-56), no CPU compute path, backend probe, length buckets."""
+
+import pytest
+import torch
+
+from tattn import attention, hip_available, triton_available
+from tattn.api import _bucket, _resolve
+from tattn import _lib
+
+
+def test_rejects_bad_inputs():
+    """The reference's test_rejects_bad_inputs (tests/test_attention.py:67-77)."""
+    x = torch.zeros(1, 1, 8, 16)
+    with pytest.raises(ValueError, match="equal shape"):
+        attention(x, x[..., :4, :], x)
+    with pytest.raises(ValueError, match="head dim"):
+        y = torch.zeros(1, 1, 8, 24)
+        attention(y, y, y)
+    with pytest.raises(ValueError, match="dtype"):
+        attention(x, x.double(), x)
+    with pytest.raises(ValueError, match="equal shape"):
+        attention(x[0], x[0], x[0])
+
+
+def test_rejects_mixed_devices():
+    """tests/test_attention.py:134-137."""
+    x = torch.zeros(1, 1, 8, 16)
+    with pytest.raises(ValueError, match="one device"):
+        attention(x, x.to("meta"), x)
+
+
+def test_rejects_bfloat16_and_mixed_dtypes():
+    x = torch.zeros(1, 1, 8, 16)
+    with pytest.raises(ValueError, match="dtype"):
+        attention(x.bfloat16(), x.bfloat16(), x.bfloat16())
+    with pytest.raises(ValueError, match="dtype"):
+        attention(x.half(), x, x)
+
+
+def test_cpu_tensors_are_refused_not_computed():
+    """The product has no CPU path: valid CPU inputs raise instead of silently computing."""
+    x = torch.zeros(1, 1, 8, 16)
+    with pytest.raises(RuntimeError, match="gfx950"):
+        attention(x, x, x)
+
+
+def test_backend_probe_false_on_cpu():
+    assert not hip_available(torch.device("cpu"))
+    assert not triton_available(torch.device("cpu"))
+
+
+def test_bucket_matches_reference_rule():
+    assert [_bucket(n) for n in (1, 2, 3, 17, 64, 65, 16384)] == [1, 2, 4, 32, 64, 128, 16384]
+
+
+def test_config_resolution():
+    assert _resolve(_lib.K_FWD, 64, torch.float16, None, False, 128) == -1
+    assert _resolve(_lib.K_FWD, 64, torch.float16, 3, False, 128) == 3
+    assert _resolve(_lib.K_FWD, 64, torch.float16, {"id": 2}, False, 128) == 2
+    first = _lib.config_desc(_lib.K_FWD, 64, _lib.F16, 0)
+    sel = {"BLOCK_M": first["block_m"], "BLOCK_N": first["block_n"], "waves": first["waves"]}
+    assert _resolve(_lib.K_FWD, 64, torch.float16, sel, False, 128) == 0
+    with pytest.raises(ValueError, match="matches 0"):
+        _resolve(_lib.K_FWD, 64, torch.float16, {"BLOCK_M": 7}, False, 128)

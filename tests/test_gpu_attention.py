@@ -1,0 +1,225 @@
+"""The reference's correctness suite (tests/test_attention.py) against the HIP kernels, plus the
+committed float64 fixtures, M checked directly, special cases and determinism.
+
+Tolerances: the reference's own (fp16 2e-2, fp32 2e-4) where its tests use them, and the tighter
+envelope the port is held to (fp16 output and gradients 2e-3, fp32 1e-5) everywhere else."""
+
+import math
+
+import pytest
+import torch
+
+from helpers import golden, rand
+from oracle import exact
+from oracle.reference import LOG2E, naive_attention
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+SHAPES = [(1, 1, 1, 16), (1, 2, 17, 16), (2, 1, 33, 32), (1, 1, 64, 64), (1, 2, 70, 16)]
+F16_TOL = {"atol": 2e-3, "rtol": 2e-3}
+F32_TOL = {"atol": 1e-5, "rtol": 1e-5}
+
+
+def tol(dtype):
+    return F16_TOL if dtype == torch.float16 else F32_TOL
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from tattn import hip_available
+
+    # On a GPU box the HIP library must load and run: never skip silently there.
+    assert hip_available(DEV), "libtattn_hip.so did not load or the device is not a gfx950"
+
+
+def r(shape, dtype, seed):
+    return rand(shape, dtype, seed, DEV)
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_forward_matches_definition(shape, causal, dtype):
+    from tattn import attention
+
+    q, k, v = (r(shape, dtype, s) for s in (1, 2, 3))
+    got = attention(q, k, v, causal=causal)
+    want = naive_attention(q.float(), k.float(), v.float(), causal=causal)
+    assert got.dtype == dtype and got.shape == q.shape
+    torch.testing.assert_close(got.float(), want, **tol(dtype))
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_gradients_match_autograd(shape, causal, dtype):
+    from tattn import attention
+
+    q, k, v = (r(shape, dtype, s).requires_grad_() for s in (4, 5, 6))
+    do = r(shape, dtype, 7)
+    attention(q, k, v, causal=causal).backward(do)
+    got = [t.grad.float() for t in (q, k, v)]
+    qr, kr, vr = (t.detach().float().requires_grad_() for t in (q, k, v))
+    naive_attention(qr, kr, vr, causal=causal).backward(do.float())
+    for g, w in zip(got, (qr.grad, kr.grad, vr.grad)):
+        torch.testing.assert_close(g, w, **tol(dtype))
+
+
+def test_custom_scale_and_noncontiguous_inputs():
+    from tattn import attention
+
+    q = r((1, 20, 2, 32), torch.float32, 9).transpose(1, 2)
+    k = r((1, 20, 2, 32), torch.float32, 10).transpose(1, 2)
+    v = r((1, 20, 2, 32), torch.float32, 11).transpose(1, 2)
+    assert not q.is_contiguous()
+    got = attention(q, k, v, sm_scale=0.3)
+    torch.testing.assert_close(got, naive_attention(q, k, v, sm_scale=0.3), **F32_TOL)
+
+
+def test_backward_with_noncontiguous_inputs_and_grad():
+    from tattn import attention
+
+    q, k, v, do = (r((1, 21, 2, 16), torch.float32, s).transpose(1, 2) for s in (20, 21, 22, 23))
+    qs, ks, vs = (t.clone().requires_grad_() for t in (q, k, v))
+    attention(qs, ks, vs, causal=True).backward(do)
+    qr, kr, vr = (t.clone().requires_grad_() for t in (q, k, v))
+    naive_attention(qr, kr, vr, causal=True).backward(do)
+    for g, w in zip((qs.grad, ks.grad, vs.grad), (qr.grad, kr.grad, vr.grad)):
+        torch.testing.assert_close(g, w, **F32_TOL)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_head_dim_128(causal):
+    from tattn import attention
+
+    q, k, v = (r((1, 1, 19, 128), torch.float16, s).requires_grad_() for s in (30, 31, 32))
+    out = attention(q, k, v, causal=causal)
+    torch.testing.assert_close(
+        out.float(), naive_attention(q.float(), k.float(), v.float(), causal=causal), **F16_TOL
+    )
+    out.sum().backward()
+    assert q.grad is not None and torch.isfinite(q.grad.float()).all()
+    qr, kr, vr = (t.detach().float().requires_grad_() for t in (q, k, v))
+    naive_attention(qr, kr, vr, causal=causal).sum().backward()
+    for g, w in zip((q.grad, k.grad, v.grad), (qr.grad, kr.grad, vr.grad)):
+        torch.testing.assert_close(g.float(), w, **F16_TOL)
+
+
+def test_double_backward_is_refused_not_wrong():
+    from tattn import attention
+
+    q, k, v = (r((1, 1, 8, 16), torch.float32, s).requires_grad_() for s in (40, 41, 42))
+    (dq,) = torch.autograd.grad(attention(q, k, v).sum(), q, create_graph=True)
+    with pytest.raises(RuntimeError):
+        torch.autograd.grad(dq.sum(), k)
+
+
+def test_backend_selection():
+    from tattn import hip_available, triton_available
+
+    assert triton_available(DEV) and hip_available(DEV)
+    assert not triton_available(torch.device("cpu"))
+
+
+# ---- committed float64 fixtures -----------------------------------------------------------
+
+FIX = [(n, d, c) for n in (1, 17, 33, 70) for d in (16, 32, 64) for c in (0, 1)]
+
+
+@pytest.mark.parametrize("n,d,causal", FIX)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_matches_float64_fixture(n, d, causal, dtype):
+    from tattn.api import _backward, _forward
+
+    g = golden()
+    tag, ctag = f"n{n}_d{d}", f"n{n}_d{d}_c{causal}"
+    q, k, v, do = (torch.from_numpy(g[f"{tag}_{x}"]).to(DEV, dtype) for x in ("q", "k", "v", "do"))
+    scale = 1.0 / math.sqrt(d)
+    o, m = _forward(q, k, v, bool(causal), scale)
+    t = tol(dtype)
+    want = lambda name: torch.from_numpy(g[f"{ctag}_{name}"]).to(DEV)  # noqa: E731
+    torch.testing.assert_close(o.float(), want("o"), **t)
+    torch.testing.assert_close(m, want("m"), atol=1e-5 if dtype == torch.float32 else 2e-3, rtol=1e-5)
+    grads = _backward(q, k, v, o, m, do, bool(causal), scale)
+    for name, got in zip(("dq", "dk", "dv"), grads):
+        torch.testing.assert_close(got.float(), want(name), **t)
+
+
+# ---- M, special cases, determinism ------------------------------------------------------------
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_m_is_base2_logsumexp(causal):
+    from tattn.api import _forward
+
+    q, k, v = (r((2, 3, 300, 64), torch.float16, s) for s in (50, 51, 52))
+    _, m = _forward(q, k, v, causal, 0.125)
+    _, want = exact.attention_fwd(q.cpu().double().numpy(), k.cpu().double().numpy(),
+                                  v.cpu().double().numpy(), causal, 0.125)
+    torch.testing.assert_close(m.cpu().double(), torch.from_numpy(want), atol=2e-5, rtol=2e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("causal", [False, True])
+def test_single_key(dtype, causal):
+    from tattn import attention
+
+    q, k, v = (r((2, 3, 1, 64), dtype, s).requires_grad_() for s in (60, 61, 62))
+    do = r((2, 3, 1, 64), dtype, 63)
+    out = attention(q, k, v, causal=causal)
+    assert torch.equal(out, v.detach())
+    out.backward(do)
+    assert torch.equal(v.grad, do)
+    assert q.grad.abs().max() <= 1e-6 and k.grad.abs().max() <= 1e-6
+
+
+def test_zero_queries_give_mean_and_cumulative_mean():
+    from tattn import attention
+
+    v = r((1, 2, 150, 64), torch.float32, 70)
+    k = r((1, 2, 150, 64), torch.float32, 71)
+    q = torch.zeros_like(v)
+    torch.testing.assert_close(attention(q, k, v), v.mean(-2, keepdim=True).expand_as(v), **F32_TOL)
+    cnt = torch.arange(1, 151, device=DEV, dtype=torch.float32).view(1, 1, 150, 1)
+    torch.testing.assert_close(attention(q, k, v, causal=True), v.cumsum(-2) / cnt, **F32_TOL)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_run_to_run_bitwise_identical(causal):
+    """No atomics anywhere: two runs give the same bits."""
+    from tattn.api import _backward, _forward
+
+    q, k, v, do = (r((2, 4, 777, 64), torch.float16, s) for s in (80, 81, 82, 83))
+    o1, m1 = _forward(q, k, v, causal, 0.125)
+    o2, m2 = _forward(q, k, v, causal, 0.125)
+    assert torch.equal(o1, o2) and torch.equal(m1, m2)
+    g1 = _backward(q, k, v, o1, m1, do, causal, 0.125)
+    g2 = _backward(q, k, v, o1, m1, do, causal, 0.125)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+def test_uses_current_stream():
+    """Work is enqueued on the caller's current stream (no host sync inside the call)."""
+    from tattn import attention
+
+    q, k, v = (r((1, 4, 512, 64), torch.float16, s) for s in (90, 91, 92))
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        out = attention(q, k, v)
+    s.synchronize()
+    torch.testing.assert_close(out.float(), naive_attention(q.float(), k.float(), v.float()), **F16_TOL)
+
+
+def test_one_hip_runtime_mapped():
+    """The library shares torch's HIP runtime (one libamdhip64 in the process)."""
+    from tattn import _lib
+
+    _lib.load()
+    maps = open("/proc/self/maps").read().splitlines()
+    paths = {line.split()[-1] for line in maps if "libamdhip64" in line}
+    assert len(paths) == 1, paths
+    assert any("libtattn_hip.so" in line for line in maps)

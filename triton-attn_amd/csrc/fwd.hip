@@ -1,0 +1,347 @@
+// Forward attention kernel for gfx950 (replaces src/tattn/kernels.py:57-148).
+//
+// One workgroup = NW waves = block_m = NW * QT * 32 query rows of one (z, h). Each wave owns
+// QT 32-query MFMA tiles and keeps its Q operands in registers. Keys stream in steps of BN
+// rows through a double-buffered LDS stage (K with the perm32 row order, V row-major), with
+// the next step's global loads in flight during the current step's math.
+//
+// Per step and wave:
+//   S^T = K Q^T        (A = K rows from LDS, B = Q^T from registers), C layout: lane = query
+//   online softmax     row max over the lane's 16*KT scores + one lane^32 swap; base-2
+//                      exponent with the scale folded into one FMA; float32 state
+//   O^T += V^T P^T     (A = V^T via transposed LDS reads, B = P^T straight from registers:
+//                      P is rounded to the element type first, as the reference does at
+//                      kernels.py:139)
+// Rescaling is lazy: the max used in the exponent only moves when a row's true max exceeds
+// it by more than 2^kRescaleLog2 (bounded growth of P, exact in real arithmetic because the
+// same max enters the running sum and the accumulator); M = max + log2(sum) is the base-2
+// log-sum-exp either way (kernels.py:143).
+//
+// Causal: key steps entirely above the workgroup's last row are never loaded; steps entirely
+// above a wave's last row are skipped by that wave; only steps that cross the diagonal or the
+// sequence end pay for per-element masks (kernels.py:117-131).
+#include "common.h"
+#include "launch.h"
+#include "tiles.h"
+
+namespace tattn {
+
+constexpr float kRescaleLog2 = 8.0f;
+
+template <typename T, int D, int NW, int QT, int BN>
+struct FwdCfg {
+  static constexpr int NT = NW * 64;
+  static constexpr int BM = NW * QT * 32;
+  static constexpr int SZ = (int)sizeof(T);
+  static constexpr int KPL = Elt<T>::KPL;
+  static constexpr int SK = 2 * KPL;        // k extent of one MFMA
+  static constexpr int NSD = D / SK;        // MFMA slices over d (S^T)
+  static constexpr int KT = BN / 32;        // 32-key tiles per step
+  static constexpr int DT = (D + 31) / 32;  // 32-row tiles over d (O^T)
+  static constexpr int NSK = BN / SK;       // MFMA slices over keys (O^T)
+  static constexpr int RK = D * SZ + 16;    // LDS row stride of K, bytes
+  static constexpr int RV = D * SZ + (SZ == 2 ? 32 : 16);
+  static constexpr int KBYTES = BN * RK;
+  static constexpr int STAGE = KBYTES + BN * RV;
+  static constexpr int LDS = 2 * STAGE;
+  static constexpr int EPC = 16 / SZ;       // elements per 16-byte chunk
+  static constexpr int CPR = D / EPC;       // chunks per row
+  static constexpr int CHUNKS = BN * CPR;
+  static constexpr int CPT = (CHUNKS + NT - 1) / NT;  // chunks per thread per tensor
+  static_assert(D % SK == 0 && BN % 32 == 0, "tile shape");
+};
+
+template <typename T, int D, int NW, int QT, int BN, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(const FwdParams p) {
+  using C = FwdCfg<T, D, NW, QT, BN>;
+  using E = Elt<T>;
+  using Op = typename E::Op;
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6, h2 = lane >> 5, l32 = lane & 31;
+  const int N = p.N;
+  const int zhs = p.Z * p.H;
+  const int zh = blockIdx.x % zhs;
+  int qb = blockIdx.x / zhs;
+  if (CAUSAL) qb = p.n_qblocks - 1 - qb;  // longest rows first
+  const int64_t z = zh / p.H, hh = zh % p.H;
+  const T* Q = (const T*)p.q + z * p.sq[0] + hh * p.sq[1];
+  const T* K = (const T*)p.k + z * p.sk[0] + hh * p.sk[1];
+  const T* V = (const T*)p.v + z * p.sv[0] + hh * p.sv[1];
+  T* O = (T*)p.o + z * p.so[0] + hh * p.so[1];
+  float* M = p.m + (int64_t)zh * N;
+  const int64_t sqn = p.sq[2], skn = p.sk[2], svn = p.sv[2], son = p.so[2];
+  const float c = p.c;
+
+  const int qblk = qb * C::BM;
+  const int qw0 = qblk + w * QT * 32;  // first query row of this wave
+
+  // Q^T operands: lane holds Q[q = qw0 + 32j + l32][KPL*h2 + SK*s + i].
+  Op qop[QT][C::NSD];
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    const int row = qw0 + 32 * j + l32;
+    const T* src = Q + (int64_t)(row < N ? row : 0) * sqn + C::KPL * h2;
+#pragma unroll
+    for (int s = 0; s < C::NSD; ++s) {
+      Op x = *reinterpret_cast<const Op*>(src + s * C::SK);
+      qop[j][s] = row < N ? x : E::zero();
+    }
+  }
+
+  const int hi = CAUSAL ? min(qblk + C::BM, N) : N;
+  const int nsteps = (hi + BN - 1) / BN;
+
+  // Global -> register prefetch of one K and one V step.
+  u32x4 pk[C::CPT], pv[C::CPT];
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < C::CPT; ++i) {
+      const int ch = tid + i * C::NT;
+      const int row = ch / C::CPR, col = (ch % C::CPR) * C::EPC;
+      const int key = kb + row;
+      const bool ok = (C::CHUNKS % C::NT == 0 || ch < C::CHUNKS) && key < N;
+      const int64_t kr = ok ? key : 0;
+      u32x4 a = ld16(K + kr * skn + col), b = ld16(V + kr * svn + col);
+      pk[i] = ok ? a : u32x4{0, 0, 0, 0};
+      pv[i] = ok ? b : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto lstore = [&](int buf) {
+    char* ks = smem + buf * C::STAGE;
+    char* vs = ks + C::KBYTES;
+#pragma unroll
+    for (int i = 0; i < C::CPT; ++i) {
+      const int ch = tid + i * C::NT;
+      if (C::CHUNKS % C::NT == 0 || ch < C::CHUNKS) {
+        const int row = ch / C::CPR, cb = (ch % C::CPR) * 16;
+        const int krow = (row & ~31) | perm32(row & 31);
+        st16(ks + krow * C::RK + cb, pk[i]);
+        st16(vs + row * C::RV + cb, pv[i]);
+      }
+    }
+  };
+
+  float mrow[QT], lrow[QT];
+  f32x16 acc[C::DT][QT];
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    mrow[j] = -__builtin_inff();
+    lrow[j] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < C::DT; ++u) acc[u][j] = f32x16{};
+  }
+
+  auto step = [&](const char* ks, const char* vs, int kb, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    f32x16 s[C::KT][QT];
+#pragma unroll
+    for (int t = 0; t < C::KT; ++t) {
+#pragma unroll
+      for (int j = 0; j < QT; ++j) s[t][j] = f32x16{};
+#pragma unroll
+      for (int sd = 0; sd < C::NSD; ++sd) {
+        const char* a = ks + (32 * t + l32) * C::RK + (sd * C::SK + C::KPL * h2) * C::SZ;
+        const Op kop = *reinterpret_cast<const TATTN_LDS Op*>((const TATTN_LDS char*)a);
+#pragma unroll
+        for (int j = 0; j < QT; ++j) s[t][j] = E::mfma(kop, qop[j][sd], s[t][j]);
+      }
+    }
+    if constexpr (MASK) {
+#pragma unroll
+      for (int t = 0; t < C::KT; ++t)
+#pragma unroll
+        for (int j = 0; j < QT; ++j) {
+          const int q = qw0 + 32 * j + l32;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kb + 32 * t + kappa(r, h2);
+            const bool dead = key >= N || (CAUSAL && key > q);
+            s[t][j][r] = dead ? -__builtin_inff() : s[t][j][r];
+          }
+        }
+    }
+    Op pop[QT][C::NSK];
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
+      float mx = s[0][j][0];
+#pragma unroll
+      for (int t = 0; t < C::KT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, s[t][j][r]);
+      mx = max_halves(mx);
+      const float cand = mx * c;
+      const bool upd = cand > mrow[j] + kRescaleLog2;
+      const float mnew = upd ? cand : mrow[j];
+      const float alpha = fast_exp2(mrow[j] - mnew);
+      if (__builtin_amdgcn_ballot_w64(upd)) {
+#pragma unroll
+        for (int u = 0; u < C::DT; ++u) acc[u][j] *= alpha;
+      }
+      mrow[j] = mnew;
+      const float nm = -mnew;
+      float ps = 0.0f;
+#pragma unroll
+      for (int t = 0; t < C::KT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e = fast_exp2(__builtin_fmaf(s[t][j][r], c, nm));
+          s[t][j][r] = e;
+          ps += e;
+        }
+      lrow[j] = lrow[j] * alpha + ps;
+      if constexpr (C::KPL == 8) {
+#pragma unroll
+        for (int sg = 0; sg < C::NSK; ++sg) {
+          const int t = sg >> 1, b = (sg & 1) * 8;
+          f16x8 x;
+#pragma unroll
+          for (int i = 0; i < 8; i += 2) {
+            f16x2 pr = pack_f16(s[t][j][b + i], s[t][j][b + i + 1]);
+            x[i] = pr[0];
+            x[i + 1] = pr[1];
+          }
+          pop[j][sg] = x;
+        }
+      } else {
+#pragma unroll
+        for (int sg = 0; sg < C::NSK; ++sg) pop[j][sg] = s[sg >> 4][j][sg & 15];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < C::DT; ++u) {
+#pragma unroll
+      for (int sg = 0; sg < C::NSK; ++sg) {
+        Op vop;
+        if constexpr (C::KPL == 8) {
+          const int g = lane >> 4, src = lane & 15;
+          const int mb = 32 * u + 16 * (g & 1);
+          const int kb0 = 16 * sg + 8 * (g >> 1);
+          const TATTN_LDS char* a =
+              (const TATTN_LDS char*)vs + (kb0 + (src >> 2)) * C::RV + (mb + 4 * (src & 3)) * 2;
+          const f16x4 lo = lds_read_tr(a), hi4 = lds_read_tr(a + 4 * C::RV);
+          vop = f16x8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+          if (D < 32 && mb >= D) vop = E::zero();
+        } else {
+          const int d = 32 * u + l32;
+          const int key = 32 * (sg >> 4) + kappa(sg & 15, h2);
+          vop = d < D ? *reinterpret_cast<const TATTN_LDS float*>(
+                            (const TATTN_LDS char*)vs + key * C::RV + d * 4)
+                      : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < QT; ++j) acc[u][j] = E::mfma(vop, pop[j][sg], acc[u][j]);
+      }
+    }
+  };
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int wave_last = qw0 + QT * 32 - 1;
+  for (int it = 0; it < nsteps; ++it) {
+    const int kb = it * BN;
+    if (it + 1 < nsteps) gload(kb + BN);
+    const char* ks = smem + (it & 1) * C::STAGE;
+    const char* vs = ks + C::KBYTES;
+    const bool idle = qw0 >= N || (CAUSAL && kb > wave_last);
+    if (!idle) {
+      const bool need_mask = kb + BN > N || (CAUSAL && kb + BN - 1 > qw0);
+      if (need_mask)
+        step(ks, vs, kb, std::true_type{});
+      else
+        step(ks, vs, kb, std::false_type{});
+    }
+    if (it + 1 < nsteps) lstore((it + 1) & 1);
+    __syncthreads();
+  }
+
+  // Epilogue: O = acc / l, M = m + log2(l).
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    const float lt = sum_halves(lrow[j]);
+    const float inv = 1.0f / lt;
+    const int q = qw0 + 32 * j + l32;
+    if (q < N) {
+      T* orow = O + (int64_t)q * son;
+#pragma unroll
+      for (int u = 0; u < C::DT; ++u)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = 32 * u + 8 * g + 4 * h2;
+          if (d0 < D) {
+            if constexpr (C::KPL == 8) {
+              f16x4 x;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) x[i] = (f16)(acc[u][j][4 * g + i] * inv);
+              *reinterpret_cast<f16x4*>(orow + d0) = x;
+            } else {
+              f32x4 x;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) x[i] = acc[u][j][4 * g + i] * inv;
+              *reinterpret_cast<f32x4*>(orow + d0) = x;
+            }
+          }
+        }
+      if (h2 == 0) M[q] = mrow[j] + __log2f(lt);
+    }
+  }
+}
+
+// ---- launch ------------------------------------------------------------------------------
+
+template <typename T, int D, int I>
+static int launch_fwd_entry(const FwdParams& p0, bool causal, hipStream_t st) {
+  constexpr TileEntry e = FwdTable<T, D>::e[I];
+  constexpr int BM = e.nw * e.tiles * 32;
+  FwdParams p = p0;
+  p.n_qblocks = (p.N + BM - 1) / BM;
+  const int64_t blocks = (int64_t)p.n_qblocks * p.Z * p.H;
+  if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
+  if (causal)
+    fwd_kernel<T, D, e.nw, e.tiles, e.other, true><<<dim3((unsigned)blocks), dim3(e.nw * 64), 0, st>>>(p);
+  else
+    fwd_kernel<T, D, e.nw, e.tiles, e.other, false><<<dim3((unsigned)blocks), dim3(e.nw * 64), 0, st>>>(p);
+  return check_launch("tattn_fwd");
+}
+
+template <typename T, int D, size_t... I>
+static int dispatch_fwd(int id, const FwdParams& p, bool causal, hipStream_t st, std::index_sequence<I...>) {
+  int rc = set_error(TATTN_E_CONFIG, "forward config id %d out of range [0, %d) for D=%d", id,
+                     (int)sizeof...(I), D);
+  ((id == (int)I ? (rc = launch_fwd_entry<T, D, I>(p, causal, st), 0) : 0), ...);
+  return rc;
+}
+
+template <typename T, int D>
+static int run_fwd_d(int id, const FwdParams& p, bool causal, hipStream_t st) {
+  return dispatch_fwd<T, D>(id, p, causal, st, std::make_index_sequence<FwdTable<T, D>::n>{});
+}
+
+int launch_fwd(const FwdParams& p, int D, int dtype, bool causal, int id, hipStream_t st) {
+  if (dtype == 0) {
+    switch (D) {
+      case 16: return run_fwd_d<f16, 16>(id, p, causal, st);
+      case 32: return run_fwd_d<f16, 32>(id, p, causal, st);
+      case 64: return run_fwd_d<f16, 64>(id, p, causal, st);
+      case 128: return run_fwd_d<f16, 128>(id, p, causal, st);
+    }
+  } else {
+    switch (D) {
+      case 16: return run_fwd_d<float, 16>(id, p, causal, st);
+      case 32: return run_fwd_d<float, 32>(id, p, causal, st);
+      case 64: return run_fwd_d<float, 64>(id, p, causal, st);
+      case 128: return run_fwd_d<float, 128>(id, p, causal, st);
+    }
+  }
+  return set_error(TATTN_E_ARG, "head dim must be 16, 32, 64 or 128, got %d", D);
+}
+
+int fwd_lds_bytes(int D, int dtype, const TileEntry& e) {
+  const int sz = dtype == 0 ? 2 : 4;
+  const int rk = D * sz + 16, rv = D * sz + (sz == 2 ? 32 : 16);
+  return 2 * e.other * (rk + rv);
+}
+
+}  // namespace tattn

@@ -1,0 +1,66 @@
+// gfx950 tile tables for the tattn kernels (replaces the reference's sm75 autotune lists,
+// src/tattn/kernels.py:21-54). One table per (kernel, element type, head dim); an entry is
+// {waves per workgroup, 32-row tiles per wave, block of the other dimension}.
+//
+//   forward  : block_m = waves * tiles * 32 query rows per workgroup, block_n keys per step
+//   dK/dV    : block_n = waves * tiles * 32 key rows per workgroup, block_m queries per step
+//   dQ       : block_m = waves * tiles * 32 query rows per workgroup, block_n keys per step
+//
+// Every entry is instantiated for causal and non-causal and is reachable through the C ABI
+// by index, so tests can run each one (the reference's test_configs.py:37-54 analog).
+#pragma once
+
+#include <stdint.h>
+
+namespace tattn {
+
+struct TileEntry {
+  int nw;     // waves per workgroup
+  int tiles;  // 32-row MFMA tiles per wave (queries for fwd/dQ, keys for dK/dV)
+  int other;  // keys per step (fwd, dQ) or queries per step (dK/dV)
+};
+
+// ---- forward ----------------------------------------------------------------------------
+template <typename T, int D> struct FwdTable;
+#define TATTN_TABLE(NAME, T, D, ...)                                    \
+  template <> struct NAME<T, D> {                                       \
+    static constexpr TileEntry e[] = {__VA_ARGS__};                     \
+    static constexpr int n = sizeof(e) / sizeof(e[0]);                  \
+  };
+
+TATTN_TABLE(FwdTable, _Float16, 16, {4, 2, 64}, {4, 1, 64}, {4, 1, 32}, {4, 2, 128})
+TATTN_TABLE(FwdTable, _Float16, 32, {4, 2, 64}, {4, 1, 64}, {4, 1, 32}, {4, 2, 128})
+TATTN_TABLE(FwdTable, _Float16, 64, {4, 2, 64}, {4, 1, 64}, {4, 2, 32}, {4, 1, 128}, {8, 1, 64}, {8, 2, 64})
+TATTN_TABLE(FwdTable, _Float16, 128, {4, 1, 64}, {4, 1, 32}, {8, 1, 32}, {4, 2, 32})
+TATTN_TABLE(FwdTable, float, 16, {4, 1, 32}, {4, 1, 64})
+TATTN_TABLE(FwdTable, float, 32, {4, 1, 32}, {4, 1, 64})
+TATTN_TABLE(FwdTable, float, 64, {4, 1, 32}, {4, 1, 64})
+TATTN_TABLE(FwdTable, float, 128, {4, 1, 32})
+
+}  // namespace tattn
+
+namespace tattn {
+
+// ---- backward dK/dV: {waves, key tiles per wave, queries per step} -------------------------
+template <typename T, int D> struct DkdvTable;
+TATTN_TABLE(DkdvTable, _Float16, 16, {4, 1, 64}, {4, 1, 32}, {4, 2, 32})
+TATTN_TABLE(DkdvTable, _Float16, 32, {4, 1, 64}, {4, 1, 32}, {4, 2, 32})
+TATTN_TABLE(DkdvTable, _Float16, 64, {4, 1, 64}, {4, 1, 32}, {8, 1, 64}, {4, 2, 32})
+TATTN_TABLE(DkdvTable, _Float16, 128, {4, 1, 32}, {4, 1, 64})
+TATTN_TABLE(DkdvTable, float, 16, {4, 1, 32}, {4, 1, 64})
+TATTN_TABLE(DkdvTable, float, 32, {4, 1, 32}, {4, 1, 64})
+TATTN_TABLE(DkdvTable, float, 64, {4, 1, 32})
+TATTN_TABLE(DkdvTable, float, 128, {4, 1, 32})
+
+// ---- backward dQ: {waves, query tiles per wave, keys per step} ------------------------------
+template <typename T, int D> struct DqTable;
+TATTN_TABLE(DqTable, _Float16, 16, {4, 2, 32}, {4, 1, 64}, {4, 1, 32})
+TATTN_TABLE(DqTable, _Float16, 32, {4, 2, 32}, {4, 1, 64}, {4, 1, 32})
+TATTN_TABLE(DqTable, _Float16, 64, {4, 2, 32}, {4, 1, 64}, {4, 1, 32}, {8, 1, 64})
+TATTN_TABLE(DqTable, _Float16, 128, {4, 1, 32}, {4, 1, 64})
+TATTN_TABLE(DqTable, float, 16, {4, 1, 32}, {4, 1, 64})
+TATTN_TABLE(DqTable, float, 32, {4, 1, 32}, {4, 1, 64})
+TATTN_TABLE(DqTable, float, 64, {4, 1, 32})
+TATTN_TABLE(DqTable, float, 128, {4, 1, 32})
+
+}  // namespace tattn

@@ -1,0 +1,204 @@
+"""Public API: `attention(q, k, v, causal=False, sm_scale=None)` with autograd.
+
+Drop-in for src/tattn/api.py of amaanmithani/triton-attn: same argument checks and messages
+(api.py:45-56), same default scale (api.py:182), same autograd contract (saves q, k, v, o, M;
+`once_differentiable` backward returning no grads for `causal` and `scale`, api.py:149-173), and
+the same internal `_forward` / `_backward` entry points with a `config=` override
+(api.py:78-146). The work runs in hand-written HIP kernels for gfx950 through the C ABI of
+libtattn_hip.so. There is no CPU path: on any device other than a ROCm gfx950 GPU the call
+raises instead of computing.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any, Union
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from tattn import _lib
+
+Config = Union[int, dict, None]
+
+_DTYPES = {torch.float16: _lib.F16, torch.float32: _lib.F32}
+
+
+def hip_available(device: torch.device) -> bool:
+    """True if `device` is a ROCm GPU this library runs on (gfx950) and the library loads."""
+    device = torch.device(device)
+    if device.type != "cuda" or torch.version.hip is None or not torch.cuda.is_available():
+        return False
+    try:
+        lib = _lib.load()
+    except (_lib.LibraryMissing, OSError):
+        return False
+    with torch.cuda.device(device):
+        return bool(lib.tattn_device_supported())
+
+
+def triton_available(device: torch.device) -> bool:
+    """The reference's backend probe (src/tattn/api.py:35-42), kept for drop-in callers: reports
+    whether the fused kernels (here: HIP for gfx950, not Triton) run on `device`."""
+    return hip_available(device)
+
+
+def _check(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    """Input validation with the reference's messages (src/tattn/api.py:45-56)."""
+    if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(
+            f"expected q, k, v of equal shape [batch, heads, seq, dim]; got {q.shape}, {k.shape}, {v.shape}"
+        )
+    if not (q.device == k.device == v.device):
+        raise ValueError(f"q, k, v must be on one device, got {q.device}, {k.device}, {v.device}")
+    d = q.shape[-1]
+    if d not in (16, 32, 64, 128):
+        raise ValueError(f"head dim must be 16, 32, 64 or 128, got {d}")
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.float16, torch.float32):
+        raise ValueError(f"q, k, v must share dtype float16 or float32, got {q.dtype}, {k.dtype}, {v.dtype}")
+
+
+def _bucket(n: int) -> int:
+    """Next power of two of a sequence length: the reference's autotune key (api.py:59-62)."""
+    return 1 << max(0, (n - 1).bit_length())
+
+
+def _require_gpu(t: torch.Tensor) -> None:
+    if not hip_available(t.device):
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"tattn runs on a ROCm gfx950 (MI355X) GPU; got tensors on {t.device}"
+            )
+        _lib.load()  # raises with the build instructions if the library is missing
+        raise RuntimeError(f"tattn: device {t.device} is not a gfx950 (MI355X) GPU")
+
+
+def _kernel_layout(t: torch.Tensor) -> torch.Tensor:
+    """The kernels read rows with 16-byte vector loads: unit d stride, 16-byte aligned rows and
+    base. Anything else is copied to a contiguous tensor (same values)."""
+    vec = 16 // t.element_size()
+    ok = (
+        t.stride(-1) == 1
+        and all(s % vec == 0 for s in t.stride()[:3])
+        and t.data_ptr() % 16 == 0
+    )
+    return t if ok else t.contiguous()
+
+
+def _resolve(kernel: int, d: int, dtype: torch.dtype, config: Config, causal: bool, n: int) -> int:
+    """Maps the reference-style `config=` to a table index: None -> the library's pick; an int is
+    the index; a dict may give "id" or any of block_m / block_n / waves / tiles (upper-case
+    BLOCK_M / BLOCK_N as in the reference are accepted) and must match exactly one entry."""
+    if config is None:
+        return -1
+    if isinstance(config, int):
+        return config
+    if "id" in config:
+        return int(config["id"])
+    want = {k.lower(): int(v) for k, v in config.items()
+            if k.lower() in ("block_m", "block_n", "waves", "tiles")}
+    code = _DTYPES[dtype]
+    hits = [c for c in range(_lib.num_configs(kernel, d, code))
+            if all(_lib.config_desc(kernel, d, code, c)[key] == val for key, val in want.items())]
+    if len(hits) != 1:
+        raise ValueError(f"config {config} matches {len(hits)} {_lib.KERNEL_NAMES[kernel]} table entries")
+    return hits[0]
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _forward(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: float,
+    config: Config = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """(O, M): O in q's layout, M = [Z, H, N] float32 base-2 log-sum-exp (api.py:78-99)."""
+    _require_gpu(q)
+    lib = _lib.load()
+    q, k, v = (_kernel_layout(t) for t in (q, k, v))
+    z, h, n, d = q.shape
+    o = torch.empty_like(q)
+    m = torch.empty((z, h, n), device=q.device, dtype=torch.float32)
+    cid = _resolve(_lib.K_FWD, d, q.dtype, config, causal, n)
+    with torch.cuda.device(q.device):
+        rc = lib.tattn_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), m.data_ptr(),
+            _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(o),
+            z, h, n, d, _DTYPES[q.dtype], int(causal), float(scale), cid, _stream(q),
+        )
+    _lib.check(rc, "tattn_fwd")
+    return o, m
+
+
+def _backward(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, m: torch.Tensor,
+    do: torch.Tensor, causal: bool, scale: float, config: Config = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dQ, dK, dV), contiguous, in the inputs' dtype (api.py:102-146). `config` is an index
+    valid in both backward tables, or a dict {"dkdv": id, "dq": id}."""
+    _require_gpu(q)
+    lib = _lib.load()
+    z, h, n, d = q.shape
+    q, k, v, do, o = (t.contiguous() for t in (q, k, v, do.to(q.dtype), o))
+    m = m.contiguous()
+    delta = torch.empty((z, h, n), device=q.device, dtype=torch.float32)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    if isinstance(config, dict) and ("dkdv" in config or "dq" in config):
+        kid = _resolve(_lib.K_BWD_DKDV, d, q.dtype, config.get("dkdv"), causal, n)
+        qid = _resolve(_lib.K_BWD_DQ, d, q.dtype, config.get("dq"), causal, n)
+    else:
+        kid = _resolve(_lib.K_BWD_DKDV, d, q.dtype, config, causal, n)
+        qid = _resolve(_lib.K_BWD_DQ, d, q.dtype, config, causal, n)
+    st = _lib.strides4(q)
+    code = _DTYPES[q.dtype]
+    stream = _stream(q)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.tattn_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta.data_ptr(), st,
+                                            z, h, n, d, code, stream), "tattn_bwd_preprocess")
+        _lib.check(lib.tattn_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+                                      dk.data_ptr(), dv.data_ptr(), m.data_ptr(), delta.data_ptr(),
+                                      st, z, h, n, d, code, int(causal), float(scale), kid, stream),
+                   "tattn_bwd_dkdv")
+        _lib.check(lib.tattn_bwd_dq(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+                                    dq.data_ptr(), m.data_ptr(), delta.data_ptr(), st, z, h, n, d,
+                                    code, int(causal), float(scale), qid, stream), "tattn_bwd_dq")
+    return dq, dk, dv
+
+
+class _Attention(torch.autograd.Function):
+    """Autograd wrapper (src/tattn/api.py:149-173)."""
+
+    @staticmethod
+    def forward(ctx: Any, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool,
+                scale: float) -> torch.Tensor:
+        o, m = _forward(q, k, v, causal, scale)
+        ctx.save_for_backward(q, k, v, o, m)
+        ctx.causal, ctx.scale = causal, scale
+        return o
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx: Any, do: torch.Tensor) -> tuple[torch.Tensor | None, ...]:
+        q, k, v, o, m = ctx.saved_tensors
+        dq, dk, dv = _backward(q, k, v, o, m, do, ctx.causal, ctx.scale)
+        return dq, dk, dv, None, None
+
+
+def attention(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
+    sm_scale: float | None = None,
+) -> torch.Tensor:
+    """Fused attention over [batch, heads, seq, dim] tensors (src/tattn/api.py:176-184):
+    softmax(q k^T * sm_scale [causal: key <= query]) v, sm_scale defaulting to 1/sqrt(dim)."""
+    _check(q, k, v)
+    scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    out: torch.Tensor = _Attention.apply(q, k, v, causal, scale)
+    return out
+
+
+def configs(kernel: str, head_dim: int, dtype: torch.dtype) -> list[dict[str, int]]:
+    """Every gfx950 tile-table entry for `kernel` in ("fwd", "bwd_dkdv", "bwd_dq")."""
+    kid = {v: k for k, v in _lib.KERNEL_NAMES.items()}[kernel]
+    code = _DTYPES[dtype]
+    return [_lib.config_desc(kid, head_dim, code, c) for c in range(_lib.num_configs(kid, head_dim, code))]

@@ -1,0 +1,233 @@
+#!/usr/bin/env python3
+"""Benchmark of the tattn attention path on one MI355X.
+
+Metric: fwd & fwd+bwd TFLOP/s (fp16, d64, H16, 16k tokens) + % of MI355X dense fp16 MFMA peak.
+Counted work follows the reference's benchmark (bench/bench.py:31-35 of amaanmithani/triton-attn):
+4*B*H*N^2*D flops per forward, halved when causal, fwd+bwd counted as 3.5x fwd.
+
+A timed step is one forward pass (non-causal, fp16) over each of the six 16,384-token shapes
+[B=16384/N, H=16, N, D=64] for N in 512..16384; inputs stay resident in HBM. `value` is the
+step's counted flops divided by its time. The same line carries the per-N sweep (forward, causal
+and non-causal; fwd+bwd, causal and non-causal, with peak extra memory), the roofline of the
+forward kernel (HIP-event kernel time on the launch stream) and a CPU baseline: the oracle's
+tiled forward timed on the host cores on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "triton-attn_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "fwd & fwd+bwd TFLOP/s (fp16,d64,H16,16k tok) + % of MI355X fp16 MFMA peak"
+PEAK_F16_TFLOPS = 2516.6  # MI355X dense fp16 MFMA (256 CUs x 2.4 GHz x 4096 flop/clk/CU)
+TOKENS, HEADS, DIM = 16384, 16, 64
+SEQS = (512, 1024, 2048, 4096, 8192, 16384)
+
+
+def flops(b: int, h: int, n: int, d: int, causal: bool, mode: str) -> float:
+    f = 4.0 * b * h * n * n * d
+    if causal:
+        f *= 0.5
+    return f * (3.5 if mode == "fwd+bwd" else 1.0)
+
+
+def _inputs(n: int, dev):
+    import torch
+
+    b = TOKENS // n
+    g = torch.Generator(device=dev).manual_seed(n)
+    q, k, v, do = (torch.randn(b, HEADS, n, DIM, device=dev, dtype=torch.float16, generator=g)
+                   for _ in range(4))
+    return b, q, k, v, do
+
+
+def _event_ms(fn, reps: int) -> float:
+    """Average ms per call of `fn` between two events on the current stream (the stream the
+    library launches on), after one untimed call."""
+    import torch
+
+    fn()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline() -> dict:
+    """The oracle's tiled forward (restatement of the reference's CPU path) on the host CPU."""
+    import torch
+
+    from oracle.reference import tiled_forward
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    b, h, n, d = 1, 4, 8192, DIM
+    g = torch.Generator().manual_seed(8192)
+    q, k, v = (torch.randn(b, h, n, d, generator=g).half() for _ in range(3))
+    run = lambda: tiled_forward(q, k, v, False, None, block_m=128, block_n=128)  # noqa: E731
+    run()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    return {
+        "value": flops(b, h, n, d, False, "fwd") / sec / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle tiled_forward (fp32 math on fp16 inputs), [B={b},H={h},N={n},D={d}] non-causal, "
+                  f"128x128 blocks, median of 3 after 1 warm-up, {sec:.3f} s per run",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--reps", type=int, default=10, help="calls per sweep cell")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true", help="only the headline forward step")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (the attention path has no multi-GPU part); got --gpus {a.gpus}",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from tattn import attention, hip_available
+    from tattn.api import _forward
+
+    dev = torch.device("cuda:0")
+    if not hip_available(dev):
+        raise RuntimeError("tattn HIP library not usable on cuda:0")
+    torch.cuda.set_device(dev)
+    data = {n: _inputs(n, dev) for n in SEQS}
+    scale = 1.0 / math.sqrt(DIM)
+
+    # ---- headline: forward over the six shapes ------------------------------------------
+    def step() -> None:
+        for n in SEQS:
+            _, q, k, v, _ = data[n]
+            _forward(q, k, v, False, scale)
+
+    step_flops = sum(flops(data[n][0], HEADS, n, DIM, False, "fwd") for n in SEQS)
+    with torch.inference_mode():
+        for _ in range(a.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / a.steps
+    value = step_flops / (ms_per_step * 1e-3) / 1e12
+
+    # ---- roofline of the forward kernel: event-timed launches of each shape -------------
+    fwd_ms = {}
+    with torch.inference_mode():
+        for n in SEQS:
+            _, q, k, v, _ = data[n]
+            fwd_ms[n] = _event_ms(lambda: _forward(q, k, v, False, scale), a.reps)
+    kernel_ms = sum(fwd_ms.values()) / len(SEQS)  # average launch duration over the step
+    achieved = step_flops / len(SEQS) / (kernel_ms * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / PEAK_F16_TFLOPS, "traffic": None,
+                "kernel": "tattn::fwd_kernel (fp16, D=64, non-causal)",
+                "avg_launch_ms": kernel_ms, "flops_per_launch": step_flops / len(SEQS)}
+
+    # ---- sweep: per N, forward and fwd+bwd, causal and non-causal -------------------------
+    sweep = []
+    agg = {}
+    if not a.no_sweep:
+        for causal in (False, True):
+            for mode in ("fwd", "fwd+bwd"):
+                tot_f = tot_ms = 0.0
+                for n in SEQS:
+                    b, q, k, v, do = data[n]
+                    if mode == "fwd":
+                        with torch.inference_mode():
+                            ms = _event_ms(lambda: attention(q, k, v, causal=causal), a.reps)
+                        peak_mib = None
+                    else:
+                        qg, kg, vg = (t.detach().clone().requires_grad_() for t in (q, k, v))
+
+                        def fb() -> None:
+                            qg.grad = kg.grad = vg.grad = None
+                            attention(qg, kg, vg, causal=causal).backward(do)
+
+                        fb()
+                        qg.grad = kg.grad = vg.grad = None
+                        torch.cuda.synchronize()
+                        torch.cuda.reset_peak_memory_stats()
+                        base = torch.cuda.memory_allocated()
+                        fb()
+                        torch.cuda.synchronize()
+                        peak_mib = (torch.cuda.max_memory_allocated() - base) / 2**20
+                        ms = _event_ms(fb, a.reps)
+                        del qg, kg, vg
+                    f = flops(b, HEADS, n, DIM, causal, mode)
+                    tf = f / (ms * 1e-3) / 1e12
+                    tot_f += f
+                    tot_ms += ms
+                    row = {"seq": n, "batch": b, "causal": causal, "mode": mode, "ms": round(ms, 4),
+                           "tflops": round(tf, 1), "pct_of_peak": round(100 * tf / PEAK_F16_TFLOPS, 2)}
+                    if peak_mib is not None:
+                        row["peak_extra_mib"] = round(peak_mib, 1)
+                    sweep.append(row)
+                    print(json.dumps(row), file=sys.stderr, flush=True)
+                key = f"{mode}_{'causal' if causal else 'non_causal'}"
+                tflops = tot_f / (tot_ms * 1e-3) / 1e12
+                agg[key] = {"tflops": round(tflops, 1), "pct_of_peak": round(100 * tflops / PEAK_F16_TFLOPS, 2)}
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic N(0,1), device generator seeded with N",
+        "config": {
+            "workload": "attention forward, fp16, non-causal, H=16, D=64, one pass over each of "
+                        "N=512,1024,2048,4096,8192,16384 with B=16384/N",
+            "tokens_per_shape": TOKENS, "heads": HEADS, "head_dim": DIM, "seqs": list(SEQS),
+        },
+        "pct_of_peak": round(100 * value / PEAK_F16_TFLOPS, 2),
+        "aggregates": agg,
+        "roofline": roofline,
+        "sweep": sweep,
+    }
+    if not a.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

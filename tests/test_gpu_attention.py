@@ -151,14 +151,19 @@ def test_matches_float64_fixture(n, d, causal, dtype):
 # ---- M, special cases, determinism ------------------------------------------------------------
 
 @pytest.mark.parametrize("causal", [False, True])
-def test_m_is_base2_logsumexp(causal):
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_m_is_base2_logsumexp(causal, dtype):
+    """M = log2(sum_j 2^(s_ij * scale * log2 e)) per row. The fp16 kernel sums the fp16-rounded
+    probabilities (the values that multiply V), so its M carries up to ~2^-11 / ln 2 of
+    rounding; the fp32 kernel sums in fp32."""
     from tattn.api import _forward
 
-    q, k, v = (r((2, 3, 300, 64), torch.float16, s) for s in (50, 51, 52))
+    q, k, v = (r((2, 3, 300, 64), dtype, s) for s in (50, 51, 52))
     _, m = _forward(q, k, v, causal, 0.125)
     _, want = exact.attention_fwd(q.cpu().double().numpy(), k.cpu().double().numpy(),
                                   v.cpu().double().numpy(), causal, 0.125)
-    torch.testing.assert_close(m.cpu().double(), torch.from_numpy(want), atol=2e-5, rtol=2e-5)
+    atol = 1e-3 if dtype == torch.float16 else 2e-5
+    torch.testing.assert_close(m.cpu().double(), torch.from_numpy(want), atol=atol, rtol=2e-5)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])

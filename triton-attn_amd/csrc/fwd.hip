@@ -20,6 +20,8 @@
 // Causal: key steps entirely above the workgroup's last row are never loaded; steps entirely
 // above a wave's last row are skipped by that wave; only steps that cross the diagonal or the
 // sequence end pay for per-element masks (kernels.py:117-131).
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 #include "tiles.h"
@@ -52,7 +54,7 @@ struct FwdCfg {
 };
 
 template <typename T, int D, int NW, int QT, int BN, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(const FwdParams p) {
+__global__ __launch_bounds__(NW * 64, 2) void fwd_generic_kernel(const FwdParams p) {
   using C = FwdCfg<T, D, NW, QT, BN>;
   using E = Elt<T>;
   using Op = typename E::Op;
@@ -162,7 +164,9 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(const FwdParams p) {
           }
         }
     }
-    Op pop[QT][C::NSK];
+    // Row max of every q-tile first, then one wave-uniform rescale branch for the whole step.
+    float mnew[QT], alpha[QT];
+    bool any_upd = false;
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
       float mx = s[0][j][0];
@@ -173,24 +177,31 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(const FwdParams p) {
       mx = max_halves(mx);
       const float cand = mx * c;
       const bool upd = cand > mrow[j] + kRescaleLog2;
-      const float mnew = upd ? cand : mrow[j];
-      const float alpha = fast_exp2(mrow[j] - mnew);
-      if (__builtin_amdgcn_ballot_w64(upd)) {
+      mnew[j] = upd ? cand : mrow[j];
+      alpha[j] = fast_exp2(mrow[j] - mnew[j]);
+      any_upd |= upd;
+    }
+    if (__builtin_amdgcn_ballot_w64(any_upd)) {
 #pragma unroll
-        for (int u = 0; u < C::DT; ++u) acc[u][j] *= alpha;
-      }
-      mrow[j] = mnew;
-      const float nm = -mnew;
-      float ps = 0.0f;
+      for (int j = 0; j < QT; ++j)
+#pragma unroll
+        for (int u = 0; u < C::DT; ++u) acc[u][j] *= alpha[j];
+    }
+    Op pop[QT][C::NSK];
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
+      mrow[j] = mnew[j];
+      const float nm = -mnew[j];
+      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int t = 0; t < C::KT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float e = fast_exp2(__builtin_fmaf(s[t][j][r], c, nm));
           s[t][j][r] = e;
-          ps += e;
+          ps[r & 3] = (t == 0 && r < 4) ? e : ps[r & 3] + e;
         }
-      lrow[j] = lrow[j] * alpha + ps;
+      lrow[j] = lrow[j] * alpha[j] + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
       if constexpr (C::KPL == 8) {
 #pragma unroll
         for (int sg = 0; sg < C::NSK; ++sg) {
@@ -289,6 +300,348 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(const FwdParams p) {
   }
 }
 
+// ---- fp16: software-pipelined forward ------------------------------------------------------
+//
+// 32 keys per step. Each step issues 16 MFMAs that do not depend on the step's softmax:
+// S_{i+1} = K_{i+1} Q^T and O^T += V_{i-1}^T P_{i-1}^T (the previous step's probabilities,
+// kept in registers), so the matrix cores stay busy while the VALU runs the softmax of step i.
+// The accumulator rescale for step i (rare, see kRescaleLog2) follows the PV of step i-1.
+// LDS ring: K tiles double-buffered (step i reads K_{i+1}, refills K[i%2] with K_{i+2}),
+// V tiles triple-buffered (step i reads V_{i-1}, refills V[(i+1)%3] with V_{i+1}); one
+// barrier per step. Tiles are read from HBM with range-checked buffer loads: rows past the
+// sequence end come back as zeros.
+// LDS row strides: K rows D*2+16 bytes (16 consecutive rows of a 16-byte column hit distinct
+// banks); V rows are an odd multiple of 64 bytes so each transposed read (4 rows x 64 bytes per
+// 32 lanes) covers distinct banks of gfx950's 64-bank LDS.
+
+template <int D>
+struct PipeLayout {
+  static constexpr int RK = D * 2 + 16;
+  static constexpr int RV = D == 16 ? 64 : D == 32 ? 64 : D == 64 ? 192 : 320;
+  static constexpr int KTILE = 32 * RK;
+  static constexpr int VTILE = 32 * RV;
+  static constexpr int NVBUF = 4;
+  static constexpr int LDS = 2 * KTILE + NVBUF * VTILE;
+};
+
+// Bytes spanned by rows [0, N) of a row-strided slice: every offset of a valid element is below
+// it and every offset of row N or later is at or above it.
+__host__ __device__ inline uint64_t slice_bytes(int64_t N, int64_t row_stride, int64_t D) {
+  return (uint64_t)((N - 1) * row_stride + D) * 2;
+}
+
+// Range-checked 16-byte row loads from one (z, h) slice, 32 rows per step: the descriptor of
+// step s starts s*32 rows in and covers the rest of the slice, so rows past the sequence end
+// read as zero. Base and size stay wave-uniform (scalar registers).
+__device__ __forceinline__ uint32_t uniform32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
+}
+
+// Range-checked buffer descriptor over rows [0, N) of one (z, h) slice: 16-byte loads at byte
+// offsets at or past the slice size read as zero, so rows past the sequence end need no
+// masking. Built once per workgroup from wave-uniform values (the descriptor must live in
+// scalar registers; offsets vary per lane and per step).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const void* base, uint64_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  const uint64_t ua = ((uint64_t)uniform32((uint32_t)(a >> 32)) << 32) | uniform32((uint32_t)a);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)ua, (short)0, (int)uniform32((uint32_t)bytes), 0x00020000);
+}
+__device__ __forceinline__ u32x4 rsrc_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+template <int D, int NW, int QT, int OCC, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams p) {
+  using L = PipeLayout<D>;
+  constexpr int NT = NW * 64, BM = NW * QT * 32;
+  constexpr int NSD = D / 16;        // 16-wide d slices of S = K Q^T
+  constexpr int DT = (D + 31) / 32;  // 32-row d tiles of O^T
+  constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
+  constexpr int CHUNKS = 32 * CPR;
+  constexpr int CPT = (CHUNKS + NT - 1) / NT;
+  __shared__ __attribute__((aligned(16))) char smem[L::LDS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6, h2 = lane >> 5, l32 = lane & 31;
+  const int N = p.N;
+  const int zhs = p.Z * p.H;
+  const int zh = blockIdx.x % zhs;
+  int qb = blockIdx.x / zhs;
+  if (CAUSAL) qb = p.n_qblocks - 1 - qb;  // longest rows first
+  const int64_t z = zh / p.H, hh = zh % p.H;
+  const f16* Q = (const f16*)p.q + z * p.sq[0] + hh * p.sq[1];
+  f16* O = (f16*)p.o + z * p.so[0] + hh * p.so[1];
+  float* M = p.m + (int64_t)zh * N;
+  const int64_t sqn = p.sq[2], son = p.so[2];
+  const __amdgpu_buffer_rsrc_t krs = slice_rsrc((const f16*)p.k + z * p.sk[0] + hh * p.sk[1], slice_bytes(N, p.sk[2], D));
+  const __amdgpu_buffer_rsrc_t vrs = slice_rsrc((const f16*)p.v + z * p.sv[0] + hh * p.sv[1], slice_bytes(N, p.sv[2], D));
+  const uint32_t k_step = uniform32((uint32_t)(p.sk[2] * 64)), v_step = uniform32((uint32_t)(p.sv[2] * 64));
+  const float c = p.c;
+
+  const int qblk = qb * BM;
+  const int qw0 = qblk + w * QT * 32;
+
+  f16x8 qop[QT][NSD];
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    const int row = qw0 + 32 * j + l32;
+    const f16* src = Q + (int64_t)(row < N ? row : 0) * sqn + 8 * h2;
+#pragma unroll
+    for (int s = 0; s < NSD; ++s) {
+      const f16x8 x = *reinterpret_cast<const f16x8*>(src + 16 * s);
+      qop[j][s] = row < N ? x : f16x8{};
+    }
+  }
+
+  const int hi = CAUSAL ? min(qblk + BM, N) : N;
+  const int nsteps = (hi + 31) / 32;
+  // Steps this wave computes: every step up to the one holding its last query row.
+  const int wave_steps = qw0 >= N ? 0 : CAUSAL ? min(nsteps, (qw0 + 32 * QT - 1) / 32 + 1) : nsteps;
+
+  // This thread's chunks of a 32-row tile: byte offsets in HBM (from the step's first row) and
+  // in the LDS tile. Per-lane LDS operand addresses are fixed too; tiles differ by constants.
+  uint32_t koff[CPT], voff[CPT];
+  int kdst[CPT], vdst[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int ch = min(tid + i * NT, CHUNKS - 1);
+    const int row = ch / CPR, cb = (ch % CPR) * 16;
+    koff[i] = (uint32_t)(row * p.sk[2] * 2 + cb);
+    voff[i] = (uint32_t)(row * p.sv[2] * 2 + cb);
+    kdst[i] = perm32(row) * L::RK + cb;
+    vdst[i] = 2 * L::KTILE + row * L::RV + cb;
+  }
+  const int g = lane >> 4, src = lane & 15;
+  const int kop_off = l32 * L::RK + 16 * h2;
+  const int vop_off = 2 * L::KTILE + (8 * (g >> 1) + (src >> 2)) * L::RV + (16 * (g & 1) + 4 * (src & 3)) * 2;
+
+  u32x4 pk[CPT], pv[CPT];
+  auto gload = [&](int i) {  // K_{i+2}, V_{i+1}
+#pragma unroll
+    for (int c2 = 0; c2 < CPT; ++c2) {
+      pk[c2] = rsrc_load(krs, koff[c2] + (uint32_t)(i + 2) * k_step);
+      pv[c2] = rsrc_load(vrs, voff[c2] + (uint32_t)(i + 1) * v_step);
+    }
+  };
+  // kb_: K buffer of K_{i+2} (== i % 2); vb_: V buffer of V_{i+1} (== (i + 1) % 4)
+  auto refill = [&](int kb_, int vb_) {
+#pragma unroll
+    for (int c2 = 0; c2 < CPT; ++c2)
+      if (CHUNKS % NT == 0 || tid + c2 * NT < CHUNKS) {
+        st16(smem + kb_ * L::KTILE + kdst[c2], pk[c2]);
+        st16(smem + vb_ * L::VTILE + vdst[c2], pv[c2]);
+      }
+    __syncthreads();
+  };
+
+  // S = K Q^T for the 32-key tile in K buffer kb_ (C layout: lane = query, register r = key
+  // kappa(r, h2)).
+  auto qk = [&](f32x16* s, int kb_) {
+#pragma unroll
+    for (int j = 0; j < QT; ++j) s[j] = f32x16{};
+#pragma unroll
+    for (int sd = 0; sd < NSD; ++sd) {
+      const f16x8 kop =
+          *reinterpret_cast<const TATTN_LDS f16x8*>((const TATTN_LDS char*)smem + kb_ * L::KTILE + kop_off + 32 * sd);
+#pragma unroll
+      for (int j = 0; j < QT; ++j) s[j] = Elt<f16>::mfma(kop, qop[j][sd], s[j]);
+    }
+  };
+
+  float mrow[QT], lrow[QT];
+  f32x16 acc[DT][QT];
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    mrow[j] = -__builtin_inff();
+    lrow[j] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < DT; ++u) acc[u][j] = f32x16{};
+  }
+  const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+
+  // O^T += V^T P^T for the 32-key tile in V buffer vb_.
+  auto pv_mma = [&](const f16x8 (*pp)[2], int vb_) {
+#pragma unroll
+    for (int u = 0; u < DT; ++u) {
+#pragma unroll
+      for (int sg = 0; sg < 2; ++sg) {
+        const TATTN_LDS char* a =
+            (const TATTN_LDS char*)smem + vb_ * L::VTILE + vop_off + 16 * sg * L::RV + 64 * u;
+        const f16x4 lo = lds_read_tr(a), hi4 = lds_read_tr(a + 4 * L::RV);
+        f16x8 vop = f16x8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+        if (D < 32 && 32 * u + 16 * (g & 1) >= D) vop = f16x8{};
+#pragma unroll
+        for (int j = 0; j < QT; ++j) acc[u][j] = Elt<f16>::mfma(vop, pp[j][sg], acc[u][j]);
+      }
+    }
+  };
+
+  // Softmax of scur (keys kb..kb+31): probabilities into pc, running max and sum updated;
+  // returns whether any row of the wave raised its max (the accumulator then needs alpha).
+  auto softmax = [&](f32x16* scur, f16x8 (*pc)[2], float* alpha, int kb, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    if constexpr (MASK) {
+#pragma unroll
+      for (int j = 0; j < QT; ++j) {
+        const int q = qw0 + 32 * j + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb + kappa(r, h2);
+          scur[j][r] = (key >= N || (CAUSAL && key > q)) ? -__builtin_inff() : scur[j][r];
+        }
+      }
+    }
+    bool any_upd = false;
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
+      float mx = __builtin_fmaxf(scur[j][0], scur[j][1]);
+#pragma unroll
+      for (int r = 2; r < 16; ++r) mx = __builtin_fmaxf(mx, scur[j][r]);
+      mx = max_halves(mx);
+      const float cand = mx * c;
+      const bool upd = cand > mrow[j] + kRescaleLog2;
+      const float mnew = upd ? cand : mrow[j];
+      alpha[j] = fast_exp2(mrow[j] - mnew);
+      any_upd |= upd;
+      mrow[j] = mnew;
+      const float nm = -mnew;
+      float ps = 0.0f;
+#pragma unroll
+      for (int sg = 0; sg < 2; ++sg) {
+        f16x8 x;
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          const float e0 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i], c, nm));
+          const float e1 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i + 1], c, nm));
+          const f16x2 pr = pack_f16(e0, e1);
+          ps = __builtin_amdgcn_fdot2(pr, ones, ps, false);
+          x[i] = pr[0];
+          x[i + 1] = pr[1];
+        }
+        pc[j][sg] = x;
+      }
+      lrow[j] = lrow[j] * alpha[j] + ps;
+    }
+    return any_upd;
+  };
+  auto rescale = [&](bool any_upd, const float* alpha) {
+    if (__builtin_amdgcn_ballot_w64(any_upd)) {
+#pragma unroll
+      for (int j = 0; j < QT; ++j)
+#pragma unroll
+        for (int u = 0; u < DT; ++u) acc[u][j] *= alpha[j];
+    }
+  };
+
+  // Prologue: K_0, K_1 into K buffers 0, 1; V_0 into V buffer 0; V buffer 3 (read by step 0
+  // together with all-zero probabilities) cleared.
+  {
+#pragma unroll
+    for (int c2 = 0; c2 < CPT; ++c2) {
+      pk[c2] = rsrc_load(krs, koff[c2]);
+      pv[c2] = rsrc_load(vrs, voff[c2]);
+    }
+    u32x4 k1[CPT];
+#pragma unroll
+    for (int c2 = 0; c2 < CPT; ++c2) k1[c2] = rsrc_load(krs, koff[c2] + k_step);
+#pragma unroll
+    for (int c2 = 0; c2 < CPT; ++c2)
+      if (CHUNKS % NT == 0 || tid + c2 * NT < CHUNKS) {
+        st16(smem + kdst[c2], pk[c2]);
+        st16(smem + L::KTILE + kdst[c2], k1[c2]);
+        st16(smem + vdst[c2], pv[c2]);
+        st16(smem + 3 * L::VTILE + vdst[c2], u32x4{0, 0, 0, 0});
+      }
+    __syncthreads();
+  }
+
+  f32x16 sa[QT], sb[QT];
+  f16x8 pa[QT][2], pb[QT][2];
+#pragma unroll
+  for (int j = 0; j < QT; ++j) pa[j][0] = pa[j][1] = f16x8{};
+  if (wave_steps > 0) qk(sa, 0);
+
+  // Steps before n_full need no mask for any wave of the workgroup (all keys below the
+  // workgroup's first query row and inside the sequence): they run branch-free, four per trip
+  // so buffer indices are constants and the S / P registers swap roles without copies. Loads
+  // past the sequence end are harmless (zeros into a free buffer). Later steps mask per element
+  // and let waves above their diagonal idle.
+  const int n_full = CAUSAL ? min((qblk + 1) / 32, N / 32) : N / 32;
+
+  // Full step i with i % 4 == IV: PV of step i-1 (pprev), S of step i+1, softmax of step i.
+  auto full_step = [&](int i, f32x16* scur, f32x16* snext, const f16x8 (*pprev)[2], f16x8 (*pcur)[2],
+                       auto iv_tag) {
+    constexpr int IV = decltype(iv_tag)::value;
+    gload(i);
+    pv_mma(pprev, (IV + 3) & 3);
+    qk(snext, (IV + 1) & 1);
+    float alpha[QT];
+    const bool upd = softmax(scur, pcur, alpha, 32 * i, std::false_type{});
+    // Interleave: loads first, then one MFMA for every few VALU instructions.
+    __builtin_amdgcn_sched_group_barrier(0x020, 2 * CPT, 0);
+#pragma unroll
+    for (int k2 = 0; k2 < 8 * QT; ++k2) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+    rescale(upd, alpha);
+    refill(IV & 1, (IV + 1) & 3);
+  };
+
+  int i = 0;
+  for (; i + 3 < n_full; i += 4) {
+    full_step(i, sa, sb, pa, pb, std::integral_constant<int, 0>{});
+    full_step(i + 1, sb, sa, pb, pa, std::integral_constant<int, 1>{});
+    full_step(i + 2, sa, sb, pa, pb, std::integral_constant<int, 2>{});
+    full_step(i + 3, sb, sa, pb, pa, std::integral_constant<int, 3>{});
+  }
+  // Remaining steps (masked or not) with run-time buffer indices; state: scur = sa, pprev = pa.
+  for (; i < nsteps; ++i) {
+    gload(i);
+    if (i - 1 < wave_steps) pv_mma(pa, (i + 3) & 3);
+    if (i < wave_steps) {
+      qk(sb, (i + 1) & 1);
+      float alpha[QT];
+      const bool mask = i >= n_full;
+      const bool upd = mask ? softmax(sa, pb, alpha, 32 * i, std::true_type{})
+                            : softmax(sa, pb, alpha, 32 * i, std::false_type{});
+      rescale(upd, alpha);
+#pragma unroll
+      for (int j = 0; j < QT; ++j) {
+        sa[j] = sb[j];
+        pa[j][0] = pb[j][0];
+        pa[j][1] = pb[j][1];
+      }
+    }
+    refill(i & 1, (i + 1) & 3);
+  }
+  if (wave_steps == nsteps && nsteps > 0) pv_mma(pa, (nsteps - 1) & 3);
+
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    const float lt = sum_halves(lrow[j]);
+    const float inv = 1.0f / lt;
+    const int q = qw0 + 32 * j + l32;
+    if (q < N) {
+      f16* orow = O + (int64_t)q * son;
+#pragma unroll
+      for (int u = 0; u < DT; ++u)
+#pragma unroll
+        for (int g2 = 0; g2 < 4; ++g2) {
+          const int d0 = 32 * u + 8 * g2 + 4 * h2;
+          if (d0 < D) {
+            f16x4 x;
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2) x[i2] = (f16)(acc[u][j][4 * g2 + i2] * inv);
+            *reinterpret_cast<f16x4*>(orow + d0) = x;
+          }
+        }
+      if (h2 == 0) M[q] = mrow[j] + __log2f(lt);
+    }
+  }
+}
+
 // ---- launch ------------------------------------------------------------------------------
 
 template <typename T, int D, int I>
@@ -299,10 +652,30 @@ static int launch_fwd_entry(const FwdParams& p0, bool causal, hipStream_t st) {
   p.n_qblocks = (p.N + BM - 1) / BM;
   const int64_t blocks = (int64_t)p.n_qblocks * p.Z * p.H;
   if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
-  if (causal)
-    fwd_kernel<T, D, e.nw, e.tiles, e.other, true><<<dim3((unsigned)blocks), dim3(e.nw * 64), 0, st>>>(p);
-  else
-    fwd_kernel<T, D, e.nw, e.tiles, e.other, false><<<dim3((unsigned)blocks), dim3(e.nw * 64), 0, st>>>(p);
+  const dim3 grid((unsigned)blocks), block(e.nw * 64);
+  const bool fits32 = slice_bytes(p.N, p.sk[2], D) + (uint64_t)p.sk[2] * 128 < (1ull << 31) &&
+                      slice_bytes(p.N, p.sv[2], D) + (uint64_t)p.sv[2] * 128 < (1ull << 31);
+  if constexpr (std::is_same<T, f16>::value) {
+    static_assert(e.other == 32, "the fp16 forward runs 32 keys per step");
+    if (!fits32) {  // slices beyond 2 GiB: 64-bit addressing
+      if (causal)
+        fwd_generic_kernel<T, D, 4, 1, 64, true><<<dim3((unsigned)(((p.N + 127) / 128) * (int64_t)p.Z * p.H)), dim3(256), 0, st>>>(
+            [&] { FwdParams q = p; q.n_qblocks = (p.N + 127) / 128; return q; }());
+      else
+        fwd_generic_kernel<T, D, 4, 1, 64, false><<<dim3((unsigned)(((p.N + 127) / 128) * (int64_t)p.Z * p.H)), dim3(256), 0, st>>>(
+            [&] { FwdParams q = p; q.n_qblocks = (p.N + 127) / 128; return q; }());
+      return check_launch("tattn_fwd");
+    }
+    if (causal)
+      fwd_pipe_kernel<D, e.nw, e.tiles, e.occ, true><<<grid, block, 0, st>>>(p);
+    else
+      fwd_pipe_kernel<D, e.nw, e.tiles, e.occ, false><<<grid, block, 0, st>>>(p);
+  } else {
+    if (causal)
+      fwd_generic_kernel<T, D, e.nw, e.tiles, e.other, true><<<grid, block, 0, st>>>(p);
+    else
+      fwd_generic_kernel<T, D, e.nw, e.tiles, e.other, false><<<grid, block, 0, st>>>(p);
+  }
   return check_launch("tattn_fwd");
 }
 
@@ -339,6 +712,14 @@ int launch_fwd(const FwdParams& p, int D, int dtype, bool causal, int id, hipStr
 }
 
 int fwd_lds_bytes(int D, int dtype, const TileEntry& e) {
+  if (dtype == 0) {
+    switch (D) {
+      case 16: return PipeLayout<16>::LDS;
+      case 32: return PipeLayout<32>::LDS;
+      case 64: return PipeLayout<64>::LDS;
+      case 128: return PipeLayout<128>::LDS;
+    }
+  }
   const int sz = dtype == 0 ? 2 : 4;
   const int rk = D * sz + 16, rv = D * sz + (sz == 2 ? 32 : 16);
   return 2 * e.other * (rk + rv);

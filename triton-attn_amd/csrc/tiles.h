@@ -18,6 +18,7 @@ struct TileEntry {
   int nw;     // waves per workgroup
   int tiles;  // 32-row MFMA tiles per wave (queries for fwd/dQ, keys for dK/dV)
   int other;  // keys per step (fwd, dQ) or queries per step (dK/dV)
+  int occ;    // waves per SIMD the kernel is compiled for (register budget 512 / occ)
 };
 
 // ---- forward ----------------------------------------------------------------------------
@@ -28,14 +29,15 @@ template <typename T, int D> struct FwdTable;
     static constexpr int n = sizeof(e) / sizeof(e[0]);                  \
   };
 
-TATTN_TABLE(FwdTable, _Float16, 16, {4, 2, 64}, {4, 1, 64}, {4, 1, 32}, {4, 2, 128})
-TATTN_TABLE(FwdTable, _Float16, 32, {4, 2, 64}, {4, 1, 64}, {4, 1, 32}, {4, 2, 128})
-TATTN_TABLE(FwdTable, _Float16, 64, {4, 2, 64}, {4, 1, 64}, {4, 2, 32}, {4, 1, 128}, {8, 1, 64}, {8, 2, 64})
-TATTN_TABLE(FwdTable, _Float16, 128, {4, 1, 64}, {4, 1, 32}, {8, 1, 32}, {4, 2, 32})
-TATTN_TABLE(FwdTable, float, 16, {4, 1, 32}, {4, 1, 64})
-TATTN_TABLE(FwdTable, float, 32, {4, 1, 32}, {4, 1, 64})
-TATTN_TABLE(FwdTable, float, 64, {4, 1, 32}, {4, 1, 64})
-TATTN_TABLE(FwdTable, float, 128, {4, 1, 32})
+// fp16 forward entries run the software-pipelined kernel (32 keys per step).
+TATTN_TABLE(FwdTable, _Float16, 16, {4, 2, 32, 2}, {4, 1, 32, 2}, {8, 1, 32, 4})
+TATTN_TABLE(FwdTable, _Float16, 32, {4, 2, 32, 2}, {4, 1, 32, 2}, {8, 1, 32, 4})
+TATTN_TABLE(FwdTable, _Float16, 64, {4, 2, 32, 2}, {4, 1, 32, 2}, {8, 1, 32, 4}, {8, 2, 32, 2}, {4, 1, 32, 4})
+TATTN_TABLE(FwdTable, _Float16, 128, {4, 1, 32, 2}, {8, 1, 32, 2}, {4, 2, 32, 1})
+TATTN_TABLE(FwdTable, float, 16, {4, 1, 32, 2}, {4, 1, 64, 2})
+TATTN_TABLE(FwdTable, float, 32, {4, 1, 32, 2}, {4, 1, 64, 2})
+TATTN_TABLE(FwdTable, float, 64, {4, 1, 32, 2}, {4, 1, 64, 2})
+TATTN_TABLE(FwdTable, float, 128, {4, 1, 32, 2})
 
 }  // namespace tattn
 
@@ -43,24 +45,24 @@ namespace tattn {
 
 // ---- backward dK/dV: {waves, key tiles per wave, queries per step} -------------------------
 template <typename T, int D> struct DkdvTable;
-TATTN_TABLE(DkdvTable, _Float16, 16, {4, 1, 64}, {4, 1, 32}, {4, 2, 32})
-TATTN_TABLE(DkdvTable, _Float16, 32, {4, 1, 64}, {4, 1, 32}, {4, 2, 32})
-TATTN_TABLE(DkdvTable, _Float16, 64, {4, 1, 64}, {4, 1, 32}, {8, 1, 64}, {4, 2, 32})
-TATTN_TABLE(DkdvTable, _Float16, 128, {4, 1, 32}, {4, 1, 64})
-TATTN_TABLE(DkdvTable, float, 16, {4, 1, 32}, {4, 1, 64})
-TATTN_TABLE(DkdvTable, float, 32, {4, 1, 32}, {4, 1, 64})
-TATTN_TABLE(DkdvTable, float, 64, {4, 1, 32})
-TATTN_TABLE(DkdvTable, float, 128, {4, 1, 32})
+TATTN_TABLE(DkdvTable, _Float16, 16, {4, 1, 64, 2}, {4, 1, 32, 2}, {4, 2, 32, 2})
+TATTN_TABLE(DkdvTable, _Float16, 32, {4, 1, 64, 2}, {4, 1, 32, 2}, {4, 2, 32, 2})
+TATTN_TABLE(DkdvTable, _Float16, 64, {4, 1, 64, 2}, {4, 1, 32, 2}, {8, 1, 64, 2}, {4, 2, 32, 2})
+TATTN_TABLE(DkdvTable, _Float16, 128, {4, 1, 32, 2}, {4, 1, 64, 2})
+TATTN_TABLE(DkdvTable, float, 16, {4, 1, 32, 2}, {4, 1, 64, 2})
+TATTN_TABLE(DkdvTable, float, 32, {4, 1, 32, 2}, {4, 1, 64, 2})
+TATTN_TABLE(DkdvTable, float, 64, {4, 1, 32, 2})
+TATTN_TABLE(DkdvTable, float, 128, {4, 1, 32, 2})
 
 // ---- backward dQ: {waves, query tiles per wave, keys per step} ------------------------------
 template <typename T, int D> struct DqTable;
-TATTN_TABLE(DqTable, _Float16, 16, {4, 2, 32}, {4, 1, 64}, {4, 1, 32})
-TATTN_TABLE(DqTable, _Float16, 32, {4, 2, 32}, {4, 1, 64}, {4, 1, 32})
-TATTN_TABLE(DqTable, _Float16, 64, {4, 2, 32}, {4, 1, 64}, {4, 1, 32}, {8, 1, 64})
-TATTN_TABLE(DqTable, _Float16, 128, {4, 1, 32}, {4, 1, 64})
-TATTN_TABLE(DqTable, float, 16, {4, 1, 32}, {4, 1, 64})
-TATTN_TABLE(DqTable, float, 32, {4, 1, 32}, {4, 1, 64})
-TATTN_TABLE(DqTable, float, 64, {4, 1, 32})
-TATTN_TABLE(DqTable, float, 128, {4, 1, 32})
+TATTN_TABLE(DqTable, _Float16, 16, {4, 2, 32, 2}, {4, 1, 64, 2}, {4, 1, 32, 2})
+TATTN_TABLE(DqTable, _Float16, 32, {4, 2, 32, 2}, {4, 1, 64, 2}, {4, 1, 32, 2})
+TATTN_TABLE(DqTable, _Float16, 64, {4, 2, 32, 2}, {4, 1, 64, 2}, {4, 1, 32, 2}, {8, 1, 64, 2})
+TATTN_TABLE(DqTable, _Float16, 128, {4, 1, 32, 2}, {4, 1, 64, 2})
+TATTN_TABLE(DqTable, float, 16, {4, 1, 32, 2}, {4, 1, 64, 2})
+TATTN_TABLE(DqTable, float, 32, {4, 1, 32, 2}, {4, 1, 64, 2})
+TATTN_TABLE(DqTable, float, 64, {4, 1, 32, 2})
+TATTN_TABLE(DqTable, float, 128, {4, 1, 32, 2})
 
 }  // namespace tattn

@@ -106,6 +106,13 @@ def main() -> int:
     ap.add_argument("--reps", type=int, default=10, help="calls per sweep cell")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="only the headline forward step")
+    ap.add_argument("--seqs", default=",".join(map(str, SEQS)),
+                    help="sequence lengths of the step (16,384 tokens each); default: all six")
+    ap.add_argument("--causal", action="store_true", help="headline step with the causal mask")
+    ap.add_argument("--backward", action="store_true",
+                    help="headline step runs forward + backward (for profiling the backward kernels)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="also run a plain device copy of this many MiB, 5 times (HBM-counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (the attention path has no multi-GPU part); got --gpus {a.gpus}",
@@ -121,17 +128,38 @@ def main() -> int:
     if not hip_available(dev):
         raise RuntimeError("tattn HIP library not usable on cuda:0")
     torch.cuda.set_device(dev)
-    data = {n: _inputs(n, dev) for n in SEQS}
+    seqs = tuple(int(x) for x in a.seqs.split(","))
+    data = {n: _inputs(n, dev) for n in (seqs if a.no_sweep else sorted(set(SEQS) | set(seqs)))}
     scale = 1.0 / math.sqrt(DIM)
+    head_mode = "fwd+bwd" if a.backward else "fwd"
 
-    # ---- headline: forward over the six shapes ------------------------------------------
-    def step() -> None:
-        for n in SEQS:
+    if a.copy_mib:
+        src = torch.empty(a.copy_mib * 2**18, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    # ---- headline: forward (or fwd+bwd) over the step's shapes ---------------------------
+    grads = {}
+    if a.backward:
+        for n in seqs:
             _, q, k, v, _ = data[n]
-            _forward(q, k, v, False, scale)
+            grads[n] = tuple(t.detach().clone().requires_grad_() for t in (q, k, v))
 
-    step_flops = sum(flops(data[n][0], HEADS, n, DIM, False, "fwd") for n in SEQS)
-    with torch.inference_mode():
+    def step() -> None:
+        for n in seqs:
+            _, q, k, v, do = data[n]
+            if a.backward:
+                qg, kg, vg = grads[n]
+                qg.grad = kg.grad = vg.grad = None
+                attention(qg, kg, vg, causal=a.causal).backward(do)
+            else:
+                _forward(q, k, v, a.causal, scale)
+
+    step_flops = sum(flops(data[n][0], HEADS, n, DIM, a.causal, head_mode) for n in seqs)
+    with torch.inference_mode(not a.backward):
         for _ in range(a.warmup):
             step()
         torch.cuda.synchronize()
@@ -145,16 +173,18 @@ def main() -> int:
 
     # ---- roofline of the forward kernel: event-timed launches of each shape -------------
     fwd_ms = {}
+    fwd_flops = 0.0
     with torch.inference_mode():
-        for n in SEQS:
+        for n in seqs:
             _, q, k, v, _ = data[n]
-            fwd_ms[n] = _event_ms(lambda: _forward(q, k, v, False, scale), a.reps)
-    kernel_ms = sum(fwd_ms.values()) / len(SEQS)  # average launch duration over the step
-    achieved = step_flops / len(SEQS) / (kernel_ms * 1e-3) / 1e12
+            fwd_ms[n] = _event_ms(lambda: _forward(q, k, v, a.causal, scale), a.reps)
+            fwd_flops += flops(data[n][0], HEADS, n, DIM, a.causal, "fwd")
+    kernel_ms = sum(fwd_ms.values()) / len(seqs)  # average launch duration over the step
+    achieved = fwd_flops / len(seqs) / (kernel_ms * 1e-3) / 1e12
     roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                 "frac": achieved / PEAK_F16_TFLOPS, "traffic": None,
-                "kernel": "tattn::fwd_kernel (fp16, D=64, non-causal)",
-                "avg_launch_ms": kernel_ms, "flops_per_launch": step_flops / len(SEQS)}
+                "kernel": f"tattn::fwd_pipe_kernel (fp16, D=64, {'causal' if a.causal else 'non-causal'})",
+                "avg_launch_ms": kernel_ms, "flops_per_launch": fwd_flops / len(seqs)}
 
     # ---- sweep: per N, forward and fwd+bwd, causal and non-causal -------------------------
     sweep = []
@@ -214,9 +244,9 @@ def main() -> int:
         "dtype": "fp16",
         "data": "synthetic N(0,1), device generator seeded with N",
         "config": {
-            "workload": "attention forward, fp16, non-causal, H=16, D=64, one pass over each of "
-                        "N=512,1024,2048,4096,8192,16384 with B=16384/N",
-            "tokens_per_shape": TOKENS, "heads": HEADS, "head_dim": DIM, "seqs": list(SEQS),
+            "workload": f"attention {head_mode}, fp16, {'causal' if a.causal else 'non-causal'}, H=16, D=64, "
+                        f"one pass over each of N={','.join(map(str, seqs))} with B=16384/N",
+            "tokens_per_shape": TOKENS, "heads": HEADS, "head_dim": DIM, "seqs": list(seqs),
         },
         "pct_of_peak": round(100 * value / PEAK_F16_TFLOPS, 2),
         "aggregates": agg,

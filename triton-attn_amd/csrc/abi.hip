@@ -97,10 +97,20 @@ const TileEntry* config_entry(int kernel, int64_t D, int dtype, int id) {
   return nullptr;
 }
 
-// Table pick for a problem (index into the kernel's table). Entry 0 of each table is its
-// general-purpose tile; the rest are alternatives reachable by explicit id.
+// Table pick for a problem (index into the kernel's table), keyed like the reference's autotuner
+// on (sequence length, head dim, causal) (src/tattn/kernels.py:57-61), but static: the choices
+// below are the fastest entries measured on an MI355X at 16,384 tokens per batch, H=16. Entry 0
+// of each table is its general-purpose tile.
 int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N) {
-  (void)kernel; (void)D; (void)dtype; (void)causal; (void)N;
+  if (dtype != TATTN_F16 || D != 64) return 0;
+  switch (kernel) {
+    case TATTN_K_FWD:  // {4,2,32} up to 2k keys, {8,2,32} (512 rows) beyond; causal favours 128 rows
+      if (causal) return N >= 8192 ? 3 : 1;
+      return N >= 4096 ? 3 : 0;
+    case TATTN_K_BWD_DKDV:  // pipelined, 4 waves (128 keys) or 8 waves (256 keys)
+    case TATTN_K_BWD_DQ:
+      return N >= 2048 ? 1 : 0;
+  }
   return 0;
 }
 

@@ -17,6 +17,9 @@
 //   dQ^T += K^T dS^T          (A = K^T through transposed LDS reads, B = dS^T registers)
 // P and dS are rounded to the element type only as MFMA operands (kernels.py:225, 228, 315);
 // dK and dQ are scaled by sm_scale at the store (kernels.py:232, 319).
+#include <type_traits>
+
+#include "bwd_pipe.h"
 #include "common.h"
 #include "launch.h"
 #include "tiles.h"
@@ -62,8 +65,8 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const BwdParams p) 
 }
 
 // ---- shared tile staging ----------------------------------------------------------------
-// One step stages two [ROWS][D] tiles (rows in perm32 order inside each 32-row tile, row stride
-// R bytes) and optionally two float vectors of ROWS entries, through registers.
+// One step stages two [ROWS][D] tiles (rows in perm32 order inside each 32-row tile) and,
+// through registers, the step's M and delta entries.
 template <typename T, int D, int ROWS, int NT>
 struct Stage2 {
   static constexpr int SZ = (int)sizeof(T);
@@ -71,7 +74,7 @@ struct Stage2 {
   static constexpr int CPR = D / EPC;
   static constexpr int CHUNKS = ROWS * CPR;
   static constexpr int CPT = (CHUNKS + NT - 1) / NT;
-  static constexpr int R = D * SZ + (SZ == 2 ? 32 : 16);
+  static constexpr int R = SZ == 2 ? Swz<D>::RB : D * SZ + 16;
   static constexpr int TILE = ROWS * R;
   u32x4 a[CPT], b[CPT];
 
@@ -94,21 +97,30 @@ struct Stage2 {
       if (CHUNKS % NT == 0 || ch < CHUNKS) {
         const int row = ch / CPR, cb = (ch % CPR) * 16;
         const int prow = (row & ~31) | perm32(row & 31);
-        st16(sa + prow * R + cb, a[i]);
-        st16(sb + prow * R + cb, b[i]);
+        const int off = SZ == 2 ? Swz<D>::addr(prow, cb) : prow * R + cb;
+        st16(sa + off, a[i]);
+        st16(sb + off, b[i]);
       }
     }
   }
 };
 
-// Transposed MFMA operand (fp16) from a perm32-ordered [rows][D] LDS tile: k runs over the 16
-// rows of slice `sl` (row 16*sl + 8*h + i for lane-half h), m/n over columns 32*u + lane%32.
-__device__ __forceinline__ f16x8 tr_operand(const char* tile, int R, int sl, int u, int lane) {
+// Natural MFMA operand (fp16): 8 halves of LDS row `row` starting at half `col` (multiple of 8).
+template <int D>
+__device__ __forceinline__ f16x8 nat_operand(const char* tile, int row, int col) {
+  return *reinterpret_cast<const TATTN_LDS f16x8*>((const TATTN_LDS char*)tile + Swz<D>::addr(row, col * 2));
+}
+
+// Transposed MFMA operand (fp16) from a perm32-ordered tile: k runs over the 16 rows of slice
+// `sl` (row 16*sl + 8*h + i for lane-half h), m/n over columns 32*u + lane%32.
+template <int D>
+__device__ __forceinline__ f16x8 tr_operand(const char* tile, int sl, int u, int lane) {
   const int g = lane >> 4, src = lane & 15;
-  const int col = 32 * u + 16 * (g & 1) + 4 * (src & 3);
+  const int colb = (32 * u + 16 * (g & 1) + 4 * (src & 3)) * 2;
   const int row = 16 * sl + 4 * (g >> 1) + (src >> 2);  // perm32 maps row 16sl+8h+4j+t to 16sl+8j+4h+t
-  const TATTN_LDS char* a = (const TATTN_LDS char*)tile + row * R + col * 2;
-  const f16x4 lo = lds_read_tr(a), hi = lds_read_tr(a + 8 * R);
+  const TATTN_LDS char* base = (const TATTN_LDS char*)tile;
+  const f16x4 lo = lds_read_tr(base + Swz<D>::addr(row, colb));
+  const f16x4 hi = lds_read_tr(base + Swz<D>::addr(row + 8, colb));
   return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -221,9 +233,15 @@ __global__ __launch_bounds__(NW * 64, 2) void dkdv_kernel(const BwdParams p) {
     for (int j = 0; j < C::QT; ++j)
 #pragma unroll
       for (int sd = 0; sd < C::NSD; ++sd) {
-        const int off = (32 * j + l32) * St::R + (sd * C::SK + C::KPL * h2) * C::SZ;
-        const Op qa = *reinterpret_cast<const TATTN_LDS Op*>((const TATTN_LDS char*)qs + off);
-        const Op da = *reinterpret_cast<const TATTN_LDS Op*>((const TATTN_LDS char*)dos + off);
+        Op qa, da;
+        if constexpr (C::KPL == 8) {
+          qa = nat_operand<D>(qs, 32 * j + l32, sd * C::SK + C::KPL * h2);
+          da = nat_operand<D>(dos, 32 * j + l32, sd * C::SK + C::KPL * h2);
+        } else {
+          const int off = (32 * j + l32) * St::R + (sd * C::SK + C::KPL * h2) * C::SZ;
+          qa = *reinterpret_cast<const TATTN_LDS Op*>((const TATTN_LDS char*)qs + off);
+          da = *reinterpret_cast<const TATTN_LDS Op*>((const TATTN_LDS char*)dos + off);
+        }
 #pragma unroll
         for (int t = 0; t < KTW; ++t) {
           s[t][j] = E::mfma(qa, kop[t][sd], s[t][j]);
@@ -283,8 +301,8 @@ __global__ __launch_bounds__(NW * 64, 2) void dkdv_kernel(const BwdParams p) {
       for (int u = 0; u < C::DT; ++u) {
         Op dob, qb;
         if constexpr (C::KPL == 8) {
-          dob = tr_operand(dos, St::R, sl, u, lane);
-          qb = tr_operand(qs, St::R, sl, u, lane);
+          dob = tr_operand<D>(dos, sl, u, lane);
+          qb = tr_operand<D>(qs, sl, u, lane);
           if (D < 32 && 32 * u + 16 * ((lane >> 4) & 1) >= D) dob = qb = E::zero();
         } else {
           dob = f32_operand(dos, St::R, sl, u, lane, D);
@@ -419,9 +437,15 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_kernel(const BwdParams p) {
       for (int j = 0; j < QTW; ++j) s[t][j] = dp[t][j] = f32x16{};
 #pragma unroll
       for (int sd = 0; sd < C::NSD; ++sd) {
-        const int off = (32 * t + l32) * St::R + (sd * C::SK + C::KPL * h2) * C::SZ;
-        const Op ka = *reinterpret_cast<const TATTN_LDS Op*>((const TATTN_LDS char*)ks + off);
-        const Op va = *reinterpret_cast<const TATTN_LDS Op*>((const TATTN_LDS char*)vs + off);
+        Op ka, va;
+        if constexpr (C::KPL == 8) {
+          ka = nat_operand<D>(ks, 32 * t + l32, sd * C::SK + C::KPL * h2);
+          va = nat_operand<D>(vs, 32 * t + l32, sd * C::SK + C::KPL * h2);
+        } else {
+          const int off = (32 * t + l32) * St::R + (sd * C::SK + C::KPL * h2) * C::SZ;
+          ka = *reinterpret_cast<const TATTN_LDS Op*>((const TATTN_LDS char*)ks + off);
+          va = *reinterpret_cast<const TATTN_LDS Op*>((const TATTN_LDS char*)vs + off);
+        }
 #pragma unroll
         for (int j = 0; j < QTW; ++j) {
           s[t][j] = E::mfma(ka, qop[j][sd], s[t][j]);
@@ -470,7 +494,7 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_kernel(const BwdParams p) {
       for (int u = 0; u < C::DT; ++u) {
         Op a;
         if constexpr (C::KPL == 8) {
-          a = tr_operand(ks, St::R, sl, u, lane);
+          a = tr_operand<D>(ks, sl, u, lane);
           if (D < 32 && 32 * u + 16 * ((lane >> 4) & 1) >= D) a = E::zero();
         } else {
           a = f32_operand(ks, St::R, sl, u, lane, D);
@@ -573,6 +597,11 @@ struct Entry {
   static constexpr TileEntry e = Table<T, D>::e[I];
 };
 
+// Buffer descriptors address a (z, h) slice with 32-bit offsets (plus two steps of look-ahead).
+static bool slice_fits32(const BwdParams& p, int D) {
+  return slice_bytes(p.N, p.s[2], D) + (uint64_t)p.s[2] * 128 < (1ull << 31);
+}
+
 template <typename T, int D, int I>
 static int launch_dkdv_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   constexpr TileEntry e = DkdvTable<T, D>::e[I];
@@ -581,10 +610,28 @@ static int launch_dkdv_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   p.n_blocks = (p.N + BNK - 1) / BNK;
   const int64_t blocks = (int64_t)p.n_blocks * p.Z * p.H;
   if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
-  if (causal)
-    dkdv_kernel<T, D, e.nw, e.tiles, e.other, true><<<dim3((unsigned)blocks), dim3(e.nw * 64), 0, st>>>(p);
-  else
-    dkdv_kernel<T, D, e.nw, e.tiles, e.other, false><<<dim3((unsigned)blocks), dim3(e.nw * 64), 0, st>>>(p);
+  const dim3 grid((unsigned)blocks), block(e.nw * 64);
+  if constexpr (e.pipe == 1) {
+    static_assert(std::is_same<T, f16>::value && D <= 64 && e.tiles == 1 && e.other == 32, "pipelined dK/dV shape");
+    if (slice_fits32(p, D)) {
+      if (causal)
+        dkdv_pipe_kernel<D, e.nw, e.occ, true><<<grid, block, 0, st>>>(p);
+      else
+        dkdv_pipe_kernel<D, e.nw, e.occ, false><<<grid, block, 0, st>>>(p);
+      return check_launch("tattn_bwd_dkdv");
+    }
+    p.n_blocks = (p.N + 127) / 128;  // slices beyond 2 GiB: 64-bit addressing
+    const dim3 g2((unsigned)((int64_t)p.n_blocks * p.Z * p.H));
+    if (causal)
+      dkdv_kernel<T, D, 4, 1, 64, true><<<g2, dim3(256), 0, st>>>(p);
+    else
+      dkdv_kernel<T, D, 4, 1, 64, false><<<g2, dim3(256), 0, st>>>(p);
+  } else {
+    if (causal)
+      dkdv_kernel<T, D, e.nw, e.tiles, e.other, true><<<grid, block, 0, st>>>(p);
+    else
+      dkdv_kernel<T, D, e.nw, e.tiles, e.other, false><<<grid, block, 0, st>>>(p);
+  }
   return check_launch("tattn_bwd_dkdv");
 }
 
@@ -596,10 +643,28 @@ static int launch_dq_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   p.n_blocks = (p.N + BMQ - 1) / BMQ;
   const int64_t blocks = (int64_t)p.n_blocks * p.Z * p.H;
   if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
-  if (causal)
-    dq_kernel<T, D, e.nw, e.tiles, e.other, true><<<dim3((unsigned)blocks), dim3(e.nw * 64), 0, st>>>(p);
-  else
-    dq_kernel<T, D, e.nw, e.tiles, e.other, false><<<dim3((unsigned)blocks), dim3(e.nw * 64), 0, st>>>(p);
+  const dim3 grid((unsigned)blocks), block(e.nw * 64);
+  if constexpr (e.pipe == 1) {
+    static_assert(std::is_same<T, f16>::value && D <= 64 && e.tiles == 1 && e.other == 32, "pipelined dQ shape");
+    if (slice_fits32(p, D)) {
+      if (causal)
+        dq_pipe_kernel<D, e.nw, e.occ, true><<<grid, block, 0, st>>>(p);
+      else
+        dq_pipe_kernel<D, e.nw, e.occ, false><<<grid, block, 0, st>>>(p);
+      return check_launch("tattn_bwd_dq");
+    }
+    p.n_blocks = (p.N + 127) / 128;  // slices beyond 2 GiB: 64-bit addressing
+    const dim3 g2((unsigned)((int64_t)p.n_blocks * p.Z * p.H));
+    if (causal)
+      dq_kernel<T, D, 4, 1, 32, true><<<g2, dim3(256), 0, st>>>(p);
+    else
+      dq_kernel<T, D, 4, 1, 32, false><<<g2, dim3(256), 0, st>>>(p);
+  } else {
+    if (causal)
+      dq_kernel<T, D, e.nw, e.tiles, e.other, true><<<grid, block, 0, st>>>(p);
+    else
+      dq_kernel<T, D, e.nw, e.tiles, e.other, false><<<grid, block, 0, st>>>(p);
+  }
   return check_launch("tattn_bwd_dq");
 }
 
@@ -646,14 +711,14 @@ int launch_bwd_dq(const BwdParams& p, int D, int dtype, bool causal, int id, hip
 }
 
 int dkdv_lds_bytes(int D, int dtype, const TileEntry& e) {
-  const int sz = dtype == 0 ? 2 : 4;
-  const int r = D * sz + (sz == 2 ? 32 : 16);
+  const int r = dtype == 0 ? (D < 32 ? 64 : 2 * D) : 4 * D + 16;
+  if (e.pipe) return 4 * (2 * 32 * r + 256);
   return 2 * (2 * e.other * r + 2 * e.other * 4);
 }
 
 int dq_lds_bytes(int D, int dtype, const TileEntry& e) {
-  const int sz = dtype == 0 ? 2 : 4;
-  const int r = D * sz + (sz == 2 ? 32 : 16);
+  const int r = dtype == 0 ? (D < 32 ? 64 : 2 * D) : 4 * D + 16;
+  if (e.pipe) return 4 * (2 * 32 * r);
   return 2 * (2 * e.other * r);
 }
 

@@ -1,0 +1,512 @@
+// Software-pipelined fp16 backward kernels for gfx950 (head dims 16, 32, 64).
+//
+// Same math and rounding points as the generic kernels in bwd.hip (the reference's
+// src/tattn/kernels.py:151-321); the difference is the schedule. Each 32-row step issues
+// MFMAs that do not depend on the step's elementwise work, so the matrix cores run while the
+// VALU computes P and dS:
+//   dK/dV step i: S_{i+1} = Q K^T, dP_{i+1} = dO V^T        (next query block)
+//                 dV += P_{i-1}^T dO, dK += dS_{i-1}^T Q      (previous query block)
+//                 VALU: P_i = exp2(S_i c - M), dS_i = P_i (dP_i - delta)
+//   dQ    step i: S^T_{i+1} = K Q^T, dP^T_{i+1} = V dO^T      (next key block)
+//                 dQ^T += K_{i-1}^T dS^T_{i-1}                (previous key block)
+//                 VALU: dS^T_i
+// Tiles stream through a 4-deep LDS ring (step i reads stages i-1, i, i+1 and refills stage
+// i+2; one barrier per step); the main loops are unrolled by four so stage offsets are
+// constants. Rows are stored in perm32 order with XOR-swizzled 16-byte chunks (Swz), which
+// keeps both the natural (ds_read_b128) and the transposed (ds_read_b64_tr_b16) operand reads
+// free of bank conflicts. HBM tiles come through range-checked buffer loads: rows past the
+// sequence end read as zero.
+#pragma once
+
+#include <type_traits>
+
+#include "common.h"
+
+namespace tattn {
+
+template <int D>
+struct BwdPipe {
+  static constexpr int RB = Swz<D>::RB;
+  static constexpr int TILE = 32 * RB;
+  static constexpr int NSD = D / 16;
+  static constexpr int DT = (D + 31) / 32;
+  static constexpr int CPR = D / 8;        // 16-byte data chunks per row
+  static constexpr int CHUNKS = 32 * CPR;  // per 32-row tile
+  static constexpr int NST = 4;            // LDS ring depth
+  static constexpr int DKDV_STAGE = 2 * TILE + 256;  // Q, dO tiles + M[32], delta[32]
+  static constexpr int DQ_STAGE = 2 * TILE;          // K, V tiles
+};
+
+// Addresses (within a tile) of the two 8-byte transposed reads that build one MFMA operand
+// whose k index runs over the 16 rows of slice sl and whose m/n index is column 32u + lane%32.
+template <int D>
+__device__ __forceinline__ void tr_addrs(int sl, int u, int lane, int& a0, int& a1) {
+  const int g = lane >> 4, src = lane & 15;
+  const int colb = (32 * u + 16 * (g & 1) + 4 * (src & 3)) * 2;
+  const int row = 16 * sl + 4 * (g >> 1) + (src >> 2);  // perm32 maps row 16sl+8h+4j+t to 16sl+8j+4h+t
+  a0 = Swz<D>::addr(row, colb);
+  a1 = Swz<D>::addr(row + 8, colb);
+}
+
+__device__ __forceinline__ f16x8 tr_pair(const char* base, int a0, int a1) {
+  const f16x4 lo = lds_read_tr((const TATTN_LDS char*)base + a0);
+  const f16x4 hi = lds_read_tr((const TATTN_LDS char*)base + a1);
+  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+__device__ __forceinline__ f16x8 lds8(const char* p) {
+  return *reinterpret_cast<const TATTN_LDS f16x8*>((const TATTN_LDS char*)p);
+}
+
+template <int N> using IC = std::integral_constant<int, N>;
+
+// ---- dK / dV --------------------------------------------------------------------------------
+template <int D, int NW, int OCC, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams p) {
+  using B = BwdPipe<D>;
+  constexpr int NT = NW * 64, BNK = NW * 32;
+  constexpr int STAGE = B::DKDV_STAGE;
+  constexpr int CPT = (B::CHUNKS + NT - 1) / NT;
+  constexpr int NSD = B::NSD, DT = B::DT;
+  __shared__ __attribute__((aligned(16))) char smem[B::NST * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6, h2 = lane >> 5, l32 = lane & 31;
+  const int N = p.N;
+  const int zhs = p.Z * p.H;
+  const int zh = blockIdx.x % zhs, kbi = blockIdx.x / zhs;  // small key blocks (most work) first
+  const int64_t hoff = (int64_t)(zh / p.H) * p.s[0] + (int64_t)(zh % p.H) * p.s[1];
+  const int64_t rs = p.s[2];
+  const float c = p.c;
+  const int kblk = kbi * BNK;
+  const int kw0 = kblk + 32 * w;
+  // Causal: query blocks below this key block never see its keys (kernels.py:206-208).
+  const int lo = CAUSAL ? kblk : 0;
+  const int nsteps = (N - lo + 31) / 32;
+
+  f16x8 kop[NSD], vop[NSD];
+  {
+    const int key = kw0 + l32;
+    const int64_t off = hoff + (int64_t)(key < N ? key : 0) * rs + 8 * h2;
+#pragma unroll
+    for (int s = 0; s < NSD; ++s) {
+      const f16x8 a = *reinterpret_cast<const f16x8*>((const f16*)p.k + off + 16 * s);
+      const f16x8 b = *reinterpret_cast<const f16x8*>((const f16*)p.v + off + 16 * s);
+      kop[s] = key < N ? a : f16x8{};
+      vop[s] = key < N ? b : f16x8{};
+    }
+  }
+  f32x16 dk[DT], dv[DT];
+#pragma unroll
+  for (int u = 0; u < DT; ++u) dk[u] = dv[u] = f32x16{};
+
+  // HBM: Q, dO rows and M, delta entries from query `lo` on.
+  const __amdgpu_buffer_rsrc_t qrs = slice_rsrc((const f16*)p.q + hoff + (int64_t)lo * rs, slice_bytes(N - lo, rs, D));
+  const __amdgpu_buffer_rsrc_t ors = slice_rsrc((const f16*)p.dout + hoff + (int64_t)lo * rs, slice_bytes(N - lo, rs, D));
+  const __amdgpu_buffer_rsrc_t mrs = slice_rsrc(p.m + (int64_t)zh * N + lo, (uint64_t)(N - lo) * 4);
+  const __amdgpu_buffer_rsrc_t drs = slice_rsrc(p.delta + (int64_t)zh * N + lo, (uint64_t)(N - lo) * 4);
+  const uint32_t step_bytes = uniform32((uint32_t)(rs * 64));
+
+  uint32_t goff[CPT];
+  int ldst[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int ch = min(tid + i * NT, B::CHUNKS - 1);
+    const int row = ch / B::CPR, cb = (ch % B::CPR) * 16;
+    goff[i] = (uint32_t)(row * rs * 2 + cb);
+    ldst[i] = Swz<D>::addr(perm32(row), cb);
+  }
+  // Lanes 0-31 of wave 0 stage M, lanes 32-63 delta (one float each, range-checked per dword).
+  const bool md_loader = tid < 64;
+  const int md_dst = 2 * B::TILE + tid * 4;
+
+  int nat[NSD];
+#pragma unroll
+  for (int s = 0; s < NSD; ++s) nat[s] = Swz<D>::addr(l32, (16 * s + 8 * h2) * 2);
+  int tra[2][DT][2];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+    for (int u = 0; u < DT; ++u) tr_addrs<D>(sl, u, lane, tra[sl][u][0], tra[sl][u][1]);
+  const int mo = 2 * B::TILE + 32 * h2;  // M of queries 8*h2.. (bytes); delta at +128
+
+  u32x4 pq[CPT], pd[CPT];
+  uint32_t pm, pdl;
+  auto gload = [&](int step) {
+    const uint32_t so = (uint32_t)step * step_bytes;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      pq[i] = rsrc_load(qrs, goff[i] + so);
+      pd[i] = rsrc_load(ors, goff[i] + so);
+    }
+    const uint32_t mo4 = (uint32_t)(((tid & 31) + 32 * step) * 4);
+    pm = __builtin_amdgcn_raw_buffer_load_b32(mrs, (int)mo4, 0, 0);
+    pdl = __builtin_amdgcn_raw_buffer_load_b32(drs, (int)mo4, 0, 0);
+  };
+  auto lstore = [&](int st) {
+    char* base = smem + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+      if (B::CHUNKS % NT == 0 || tid + i * NT < B::CHUNKS) {
+        st16(base + ldst[i], pq[i]);
+        st16(base + B::TILE + ldst[i], pd[i]);
+      }
+    if (md_loader) *reinterpret_cast<uint32_t*>(base + md_dst) = (tid & 32) ? pdl : pm;
+  };
+
+  // S = Q K^T and dP = dO V^T of the stage's 32 queries (C layout: lane = key,
+  // register r = query kappa(r, h2)).
+  auto qk = [&](f32x16& s, f32x16& dp, int st) {
+    const char* base = smem + st * STAGE;
+    s = f32x16{};
+    dp = f32x16{};
+#pragma unroll
+    for (int sd = 0; sd < NSD; ++sd) {
+      s = Elt<f16>::mfma(lds8(base + nat[sd]), kop[sd], s);
+      dp = Elt<f16>::mfma(lds8(base + B::TILE + nat[sd]), vop[sd], dp);
+    }
+  };
+  // dV += P^T dO, dK += dS^T Q over the stage's 32 queries.
+  auto grad_mma = [&](const f16x8* pp, const f16x8* dsp, int st) {
+    const char* base = smem + st * STAGE;
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+      for (int u = 0; u < DT; ++u) {
+        f16x8 dob = tr_pair(base + B::TILE, tra[sl][u][0], tra[sl][u][1]);
+        f16x8 qb = tr_pair(base, tra[sl][u][0], tra[sl][u][1]);
+        if (D < 32 && 16 * ((lane >> 4) & 1) >= D) dob = qb = f16x8{};
+        dv[u] = Elt<f16>::mfma(pp[sl], dob, dv[u]);
+        dk[u] = Elt<f16>::mfma(dsp[sl], qb, dk[u]);
+      }
+  };
+  // P = exp2(S c - M), dS = P (dP - delta) for the stage's queries, rounded into MFMA operands.
+  auto pds = [&](const f32x16& s, const f32x16& dp, f16x8* pp, f16x8* dsp, int st, int q0, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const char* base = smem + st * STAGE;
+    const int key = kw0 + l32;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const f32x4 m0 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 64 * a);
+      const f32x4 m1 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 64 * a + 16);
+      const f32x4 d0 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 128 + 64 * a);
+      const f32x4 d1 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 128 + 64 * a + 16);
+      f16x8 x, y;
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        float pr[2], dr[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int r = 8 * a + i + e;
+          const float mv = (i + e) < 4 ? m0[i + e] : m1[i + e - 4];
+          const float dl = (i + e) < 4 ? d0[i + e] : d1[i + e - 4];
+          float pv = fast_exp2(__builtin_fmaf(s[r], c, -mv));
+          if constexpr (MASK) pv = key > q0 + kappa(r, h2) ? 0.0f : pv;
+          pr[e] = pv;
+          dr[e] = pv * (dp[r] - dl);
+        }
+        const f16x2 ph = pack_f16(pr[0], pr[1]), dh = pack_f16(dr[0], dr[1]);
+        x[i] = ph[0];
+        x[i + 1] = ph[1];
+        y[i] = dh[0];
+        y[i + 1] = dh[1];
+      }
+      pp[a] = x;
+      dsp[a] = y;
+    }
+  };
+
+  // Prologue: steps 0 and 1 into stages 0 and 1; stage 3 (read by step 0 together with
+  // all-zero P and dS) cleared.
+  gload(0);
+  lstore(0);
+  gload(1);
+  lstore(1);
+#pragma unroll
+  for (int i = 0; i < CPT; ++i)
+    if (B::CHUNKS % NT == 0 || tid + i * NT < B::CHUNKS) {
+      st16(smem + 3 * STAGE + ldst[i], u32x4{0, 0, 0, 0});
+      st16(smem + 3 * STAGE + B::TILE + ldst[i], u32x4{0, 0, 0, 0});
+    }
+  __syncthreads();
+
+  f32x16 sa, da, sb, db;
+  f16x8 pa[2] = {}, dsa[2] = {}, pb[2], dsb[2];
+  qk(sa, da, 0);
+
+  // One step: S/dP of step i+1, dV/dK of step i-1, P/dS of step i; ST = i % 4 (or -1: run time).
+  auto step = [&](int i, int st, f32x16& scur, f32x16& dcur, f32x16& snext, f32x16& dnext,
+                  const f16x8* pprev, const f16x8* dsprev, f16x8* pcur, f16x8* dscur, auto mask_tag) {
+    gload(i + 2);
+    qk(snext, dnext, (st + 1) & 3);
+    grad_mma(pprev, dsprev, (st + 3) & 3);
+    pds(scur, dcur, pcur, dscur, st, lo + 32 * i, mask_tag);
+    __builtin_amdgcn_sched_group_barrier(0x020, 2 * CPT + 2, 0);
+#pragma unroll
+    for (int k2 = 0; k2 < 4 * NSD; ++k2) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+    }
+    lstore((st + 2) & 3);
+    __syncthreads();
+  };
+  auto roll = [&]() {  // next becomes current
+    sa = sb;
+    da = db;
+    pa[0] = pb[0];
+    pa[1] = pb[1];
+    dsa[0] = dsb[0];
+    dsa[1] = dsb[1];
+  };
+
+  int i = 0;
+  // Causal: the workgroup's first NW query blocks cross its keys' diagonal; mask them.
+  const int n_mask = CAUSAL ? min(nsteps, NW) : 0;
+  for (; i < n_mask; ++i) {
+    step(i, i & 3, sa, da, sb, db, pa, dsa, pb, dsb, std::true_type{});
+    roll();
+  }
+  for (; i + 3 < nsteps; i += 4) {  // i % 4 == 0 here (NW is a multiple of 4)
+    step(i, 0, sa, da, sb, db, pa, dsa, pb, dsb, std::false_type{});
+    step(i + 1, 1, sb, db, sa, da, pb, dsb, pa, dsa, std::false_type{});
+    step(i + 2, 2, sa, da, sb, db, pa, dsa, pb, dsb, std::false_type{});
+    step(i + 3, 3, sb, db, sa, da, pb, dsb, pa, dsa, std::false_type{});
+  }
+  for (; i < nsteps; ++i) {
+    step(i, i & 3, sa, da, sb, db, pa, dsa, pb, dsb, std::false_type{});
+    roll();
+  }
+  grad_mma(pa, dsa, (nsteps - 1) & 3);
+
+  // Store: C register r of lane holds key 8*(r/4) + 4*h2 + r%4 of the wave, column 32u + l32.
+  f16* DK = (f16*)p.dk + hoff;
+  f16* DV = (f16*)p.dv + hoff;
+#pragma unroll
+  for (int u = 0; u < DT; ++u) {
+    const int d = 32 * u + l32;
+    if (d < D) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kw0 + 8 * (r >> 2) + 4 * h2 + (r & 3);
+        if (key < N) {
+          DK[(int64_t)key * rs + d] = (f16)(dk[u][r] * p.scale);
+          DV[(int64_t)key * rs + d] = (f16)dv[u][r];
+        }
+      }
+    }
+  }
+}
+
+// ---- dQ ----------------------------------------------------------------------------------
+template <int D, int NW, int OCC, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p) {
+  using B = BwdPipe<D>;
+  constexpr int NT = NW * 64, BMQ = NW * 32;
+  constexpr int STAGE = B::DQ_STAGE;
+  constexpr int CPT = (B::CHUNKS + NT - 1) / NT;
+  constexpr int NSD = B::NSD, DT = B::DT;
+  __shared__ __attribute__((aligned(16))) char smem[B::NST * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6, h2 = lane >> 5, l32 = lane & 31;
+  const int N = p.N;
+  const int zhs = p.Z * p.H;
+  const int zh = blockIdx.x % zhs;
+  int qb = blockIdx.x / zhs;
+  if (CAUSAL) qb = p.n_blocks - 1 - qb;  // longest rows first
+  const int64_t hoff = (int64_t)(zh / p.H) * p.s[0] + (int64_t)(zh % p.H) * p.s[1];
+  const int64_t rs = p.s[2];
+  const float c = p.c;
+  const int qblk = qb * BMQ;
+  const int qw0 = qblk + 32 * w;
+  const int q = qw0 + l32;
+
+  f16x8 qop[NSD], dop[NSD];
+  {
+    const int64_t off = hoff + (int64_t)(q < N ? q : 0) * rs + 8 * h2;
+#pragma unroll
+    for (int s = 0; s < NSD; ++s) {
+      const f16x8 a = *reinterpret_cast<const f16x8*>((const f16*)p.q + off + 16 * s);
+      const f16x8 b = *reinterpret_cast<const f16x8*>((const f16*)p.dout + off + 16 * s);
+      qop[s] = q < N ? a : f16x8{};
+      dop[s] = q < N ? b : f16x8{};
+    }
+  }
+  const float nm = -(q < N ? p.m[(int64_t)zh * N + q] : 0.0f);
+  const float dl = q < N ? p.delta[(int64_t)zh * N + q] : 0.0f;
+  f32x16 dq[DT];
+#pragma unroll
+  for (int u = 0; u < DT; ++u) dq[u] = f32x16{};
+
+  const int hi = CAUSAL ? min(qblk + BMQ, N) : N;
+  const int nsteps = (hi + 31) / 32;
+  // Steps this wave computes: every step up to the one holding its last query row.
+  const int wave_steps = qw0 >= N ? 0 : CAUSAL ? min(nsteps, (qw0 + 31) / 32 + 1) : nsteps;
+  // Steps before n_full need no mask for any wave of the workgroup.
+  const int n_full = CAUSAL ? min((qblk + 1) / 32, N / 32) : N / 32;
+
+  const __amdgpu_buffer_rsrc_t krs = slice_rsrc((const f16*)p.k + hoff, slice_bytes(N, rs, D));
+  const __amdgpu_buffer_rsrc_t vrs = slice_rsrc((const f16*)p.v + hoff, slice_bytes(N, rs, D));
+  const uint32_t step_bytes = uniform32((uint32_t)(rs * 64));
+  uint32_t goff[CPT];
+  int ldst[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int ch = min(tid + i * NT, B::CHUNKS - 1);
+    const int row = ch / B::CPR, cb = (ch % B::CPR) * 16;
+    goff[i] = (uint32_t)(row * rs * 2 + cb);
+    ldst[i] = Swz<D>::addr(perm32(row), cb);
+  }
+  int nat[NSD];
+#pragma unroll
+  for (int s = 0; s < NSD; ++s) nat[s] = Swz<D>::addr(l32, (16 * s + 8 * h2) * 2);
+  int tra[2][DT][2];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+    for (int u = 0; u < DT; ++u) tr_addrs<D>(sl, u, lane, tra[sl][u][0], tra[sl][u][1]);
+
+  u32x4 pk[CPT], pv[CPT];
+  auto gload = [&](int step) {
+    const uint32_t so = (uint32_t)step * step_bytes;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      pk[i] = rsrc_load(krs, goff[i] + so);
+      pv[i] = rsrc_load(vrs, goff[i] + so);
+    }
+  };
+  auto lstore = [&](int st) {
+    char* base = smem + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+      if (B::CHUNKS % NT == 0 || tid + i * NT < B::CHUNKS) {
+        st16(base + ldst[i], pk[i]);
+        st16(base + B::TILE + ldst[i], pv[i]);
+      }
+  };
+  // S^T = K Q^T and dP^T = V dO^T of the stage's 32 keys (C layout: lane = query,
+  // register r = key kappa(r, h2)).
+  auto qk = [&](f32x16& s, f32x16& dp, int st) {
+    const char* base = smem + st * STAGE;
+    s = f32x16{};
+    dp = f32x16{};
+#pragma unroll
+    for (int sd = 0; sd < NSD; ++sd) {
+      s = Elt<f16>::mfma(lds8(base + nat[sd]), qop[sd], s);
+      dp = Elt<f16>::mfma(lds8(base + B::TILE + nat[sd]), dop[sd], dp);
+    }
+  };
+  // dQ^T += K^T dS^T over the stage's 32 keys.
+  auto dq_mma = [&](const f16x8* dsp, int st) {
+    const char* base = smem + st * STAGE;
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+      for (int u = 0; u < DT; ++u) {
+        f16x8 a = tr_pair(base, tra[sl][u][0], tra[sl][u][1]);
+        if (D < 32 && 16 * ((lane >> 4) & 1) >= D) a = f16x8{};
+        dq[u] = Elt<f16>::mfma(a, dsp[sl], dq[u]);
+      }
+  };
+  auto dsv = [&](const f32x16& s, const f32x16& dp, f16x8* dsp, int kb, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      f16x8 x;
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        float dr[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int r = 8 * a + i + e;
+          float pv2 = fast_exp2(__builtin_fmaf(s[r], c, nm));
+          if constexpr (MASK) {
+            const int key = kb + kappa(r, h2);
+            pv2 = (key >= N || (CAUSAL && key > q)) ? 0.0f : pv2;
+          }
+          dr[e] = pv2 * (dp[r] - dl);
+        }
+        const f16x2 dh = pack_f16(dr[0], dr[1]);
+        x[i] = dh[0];
+        x[i + 1] = dh[1];
+      }
+      dsp[a] = x;
+    }
+  };
+
+  gload(0);
+  lstore(0);
+  gload(1);
+  lstore(1);
+#pragma unroll
+  for (int i = 0; i < CPT; ++i)
+    if (B::CHUNKS % NT == 0 || tid + i * NT < B::CHUNKS) st16(smem + 3 * STAGE + ldst[i], u32x4{0, 0, 0, 0});
+  __syncthreads();
+
+  f32x16 sa, da, sb, db;
+  f16x8 ea[2] = {}, eb[2];
+  if (wave_steps > 0) qk(sa, da, 0);
+
+  auto full_step = [&](int i, int st, f32x16& scur, f32x16& dcur, f32x16& snext, f32x16& dnext,
+                       const f16x8* eprev, f16x8* ecur) {
+    gload(i + 2);
+    qk(snext, dnext, (st + 1) & 3);
+    dq_mma(eprev, (st + 3) & 3);
+    dsv(scur, dcur, ecur, 32 * i, std::false_type{});
+    __builtin_amdgcn_sched_group_barrier(0x020, 2 * CPT, 0);
+#pragma unroll
+    for (int k2 = 0; k2 < 2 * NSD + 2 * DT; ++k2) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+    lstore((st + 2) & 3);
+    __syncthreads();
+  };
+
+  int i = 0;
+  for (; i + 3 < n_full; i += 4) {
+    full_step(i, 0, sa, da, sb, db, ea, eb);
+    full_step(i + 1, 1, sb, db, sa, da, eb, ea);
+    full_step(i + 2, 2, sa, da, sb, db, ea, eb);
+    full_step(i + 3, 3, sb, db, sa, da, eb, ea);
+  }
+  // Remaining steps (masked or not): state scur = sa, eprev = ea.
+  for (; i < nsteps; ++i) {
+    gload(i + 2);
+    if (i - 1 < wave_steps) dq_mma(ea, (i + 3) & 3);
+    if (i < wave_steps) {
+      qk(sb, db, (i + 1) & 3);
+      if (i >= n_full)
+        dsv(sa, da, eb, 32 * i, std::true_type{});
+      else
+        dsv(sa, da, eb, 32 * i, std::false_type{});
+      sa = sb;
+      da = db;
+      ea[0] = eb[0];
+      ea[1] = eb[1];
+    }
+    lstore((i + 2) & 3);
+    __syncthreads();
+  }
+  if (wave_steps == nsteps && nsteps > 0) dq_mma(ea, (nsteps - 1) & 3);
+
+  if (q < N) {
+    f16* row = (f16*)p.dq + hoff + (int64_t)q * rs;
+#pragma unroll
+    for (int u = 0; u < DT; ++u)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = 32 * u + 8 * g + 4 * h2;
+        if (d0 < D) {
+          f16x4 x;
+#pragma unroll
+          for (int i2 = 0; i2 < 4; ++i2) x[i2] = (f16)(dq[u][4 * g + i2] * p.scale);
+          *reinterpret_cast<f16x4*>(row + d0) = x;
+        }
+      }
+  }
+}
+
+}  // namespace tattn

@@ -131,4 +131,46 @@ struct BwdParams {
   float scale;  // sm_scale
 };
 
+// Bytes spanned by rows [0, N) of a row-strided slice: every offset of a valid element is below
+// it and every offset of row N or later is at or above it.
+__host__ __device__ inline uint64_t slice_bytes(int64_t N, int64_t row_stride, int64_t D) {
+  return (uint64_t)((N - 1) * row_stride + D) * 2;
+}
+
+// Value of lane 0 (for values the caller knows are wave-uniform: keeps them in scalar registers).
+__device__ __forceinline__ uint32_t uniform32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
+}
+
+// Range-checked buffer descriptor over rows [0, N) of one (z, h) slice: 16-byte loads at byte
+// offsets at or past the slice size read as zero, so rows past the sequence end need no
+// masking. Built once per workgroup from wave-uniform values (the descriptor must live in
+// scalar registers; offsets vary per lane and per step).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const void* base, uint64_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  const uint64_t ua = ((uint64_t)uniform32((uint32_t)(a >> 32)) << 32) | uniform32((uint32_t)a);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)ua, (short)0, (int)uniform32((uint32_t)bytes), 0x00020000);
+}
+__device__ __forceinline__ u32x4 rsrc_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+
+// fp16 tiles are stored without padding, with the 16-byte chunks of row r XOR-permuted by
+// swz(r). The permutation is chosen so that both access patterns of these tiles hit 64
+// distinct banks per 256 bytes: 16 consecutive rows read at one chunk (natural MFMA operands,
+// ds_read_b128), and 4 consecutive rows read across 4 aligned chunks (transposed operands,
+// ds_read_b64_tr_b16). D=16 rows use the D=32 geometry (64 bytes, upper half unused).
+template <int D>
+struct Swz {
+  static constexpr int RB = D < 32 ? 64 : D * 2;  // bytes per row
+  static __device__ __forceinline__ int f(int r) {
+    if constexpr (RB == 256) return ((r & 3) << 2) | ((r >> 2) & 3);
+    else if constexpr (RB == 128) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    else return (r >> 2) & 3;
+  }
+  // Byte address of byte `b` of row r (b < RB).
+  static __device__ __forceinline__ int addr(int r, int b) { return r * RB + ((((b >> 4) ^ f(r)) << 4) | (b & 15)); }
+};
+
 }  // namespace tattn

@@ -324,32 +324,6 @@ struct PipeLayout {
   static constexpr int LDS = 2 * KTILE + NVBUF * VTILE;
 };
 
-// Bytes spanned by rows [0, N) of a row-strided slice: every offset of a valid element is below
-// it and every offset of row N or later is at or above it.
-__host__ __device__ inline uint64_t slice_bytes(int64_t N, int64_t row_stride, int64_t D) {
-  return (uint64_t)((N - 1) * row_stride + D) * 2;
-}
-
-// Range-checked 16-byte row loads from one (z, h) slice, 32 rows per step: the descriptor of
-// step s starts s*32 rows in and covers the rest of the slice, so rows past the sequence end
-// read as zero. Base and size stay wave-uniform (scalar registers).
-__device__ __forceinline__ uint32_t uniform32(uint32_t x) {
-  return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
-}
-
-// Range-checked buffer descriptor over rows [0, N) of one (z, h) slice: 16-byte loads at byte
-// offsets at or past the slice size read as zero, so rows past the sequence end need no
-// masking. Built once per workgroup from wave-uniform values (the descriptor must live in
-// scalar registers; offsets vary per lane and per step).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const void* base, uint64_t bytes) {
-  const uint64_t a = (uint64_t)base;
-  const uint64_t ua = ((uint64_t)uniform32((uint32_t)(a >> 32)) << 32) | uniform32((uint32_t)a);
-  return __builtin_amdgcn_make_buffer_rsrc((void*)ua, (short)0, (int)uniform32((uint32_t)bytes), 0x00020000);
-}
-__device__ __forceinline__ u32x4 rsrc_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-}
-
 template <int D, int NW, int QT, int OCC, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams p) {
   using L = PipeLayout<D>;

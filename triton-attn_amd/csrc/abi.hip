@@ -104,9 +104,9 @@ const TileEntry* config_entry(int kernel, int64_t D, int dtype, int id) {
 int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N) {
   if (dtype != TATTN_F16 || D != 64) return 0;
   switch (kernel) {
-    case TATTN_K_FWD:  // {4,2,32} up to 2k keys, {8,2,32} (512 rows) beyond; causal favours 128 rows
-      if (causal) return N >= 8192 ? 3 : 1;
-      return N >= 4096 ? 3 : 0;
+    case TATTN_K_FWD:  // short rows: 128-row blocks; long: 256 rows (causal) or 512 rows
+      if (causal) return N >= 8192 ? 0 : 1;
+      return N >= 8192 ? 3 : N >= 2048 ? 0 : 1;
     case TATTN_K_BWD_DKDV:  // pipelined, 4 waves (128 keys) or 8 waves (256 keys)
     case TATTN_K_BWD_DQ:
       return N >= 2048 ? 1 : 0;

@@ -305,11 +305,14 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_generic_kernel(const FwdParams
 // 32 keys per step. Each step issues 16 MFMAs that do not depend on the step's softmax:
 // S_{i+1} = K_{i+1} Q^T and O^T += V_{i-1}^T P_{i-1}^T (the previous step's probabilities,
 // kept in registers), so the matrix cores stay busy while the VALU runs the softmax of step i.
-// The accumulator rescale for step i (rare, see kRescaleLog2) follows the PV of step i-1.
-// LDS ring: K tiles double-buffered (step i reads K_{i+1}, refills K[i%2] with K_{i+2}),
-// V tiles triple-buffered (step i reads V_{i-1}, refills V[(i+1)%3] with V_{i+1}); one
-// barrier per step. Tiles are read from HBM with range-checked buffer loads: rows past the
-// sequence end come back as zeros.
+// Unmasked steps skip the row max: probabilities use the running max as it stands and a
+// per-lane sum check sends the wave to a slow path (row max, rescale, S recomputed from the
+// K tile still in LDS) only when some probability could exceed 2^12, which after the first
+// step is rare. Masked steps (diagonal, sequence end) always take the full softmax.
+// LDS rings of three tiles each: step i reads K_{i+1} (and K_i on the slow path) and V_{i-1},
+// and refills K[(i+2)%3] with K_{i+2} and V[(i+1)%3] with V_{i+1}; one barrier per step.
+// Tiles are read from HBM with range-checked buffer loads: rows past the sequence end come
+// back as zeros.
 // LDS row strides: K rows D*2+16 bytes (16 consecutive rows of a 16-byte column hit distinct
 // banks); V rows are an odd multiple of 64 bytes so each transposed read (4 rows x 64 bytes per
 // 32 lanes) covers distinct banks of gfx950's 64-bank LDS.
@@ -320,8 +323,11 @@ struct PipeLayout {
   static constexpr int RV = D == 16 ? 64 : D == 32 ? 64 : D == 64 ? 192 : 320;
   static constexpr int KTILE = 32 * RK;
   static constexpr int VTILE = 32 * RV;
-  static constexpr int NVBUF = 4;
-  static constexpr int LDS = 2 * KTILE + NVBUF * VTILE;
+  // Three-deep rings: during step i the kernel reads K_{i+1} (S of the next step) and, on the
+  // rare slow softmax path, K_i, and reads V_{i-1}; it writes K_{i+2} and V_{i+1}.
+  static constexpr int NKBUF = 3, NVBUF = 3;
+  static constexpr int VBASE = NKBUF * KTILE;
+  static constexpr int LDS = VBASE + NVBUF * VTILE;
 };
 
 template <int D, int NW, int QT, int OCC, bool CAUSAL>
@@ -383,11 +389,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
     koff[i] = (uint32_t)(row * p.sk[2] * 2 + cb);
     voff[i] = (uint32_t)(row * p.sv[2] * 2 + cb);
     kdst[i] = perm32(row) * L::RK + cb;
-    vdst[i] = 2 * L::KTILE + row * L::RV + cb;
+    vdst[i] = L::VBASE + row * L::RV + cb;
   }
   const int g = lane >> 4, src = lane & 15;
   const int kop_off = l32 * L::RK + 16 * h2;
-  const int vop_off = 2 * L::KTILE + (8 * (g >> 1) + (src >> 2)) * L::RV + (16 * (g & 1) + 4 * (src & 3)) * 2;
+  const int vop_off = L::VBASE + (8 * (g >> 1) + (src >> 2)) * L::RV + (16 * (g & 1) + 4 * (src & 3)) * 2;
 
   u32x4 pk[CPT], pv[CPT];
   auto gload = [&](int i) {  // K_{i+2}, V_{i+1}
@@ -397,14 +403,19 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
       pv[c2] = rsrc_load(vrs, voff[c2] + (uint32_t)(i + 1) * v_step);
     }
   };
-  // kb_: K buffer of K_{i+2} (== i % 2); vb_: V buffer of V_{i+1} (== (i + 1) % 4)
-  auto refill = [&](int kb_, int vb_) {
+  // kb_: K buffer of K_{i+2} (== (i + 2) % 3); vb_: V buffer of V_{i+1} (== (i + 1) % 3)
+  // Unguarded: a thread past the last chunk has its chunk index clamped to the last one, so it
+  // stores the same bytes to the same address as that chunk's owner (a branch here would split
+  // the step's scheduling region).
+  auto lstore = [&](int kb_, int vb_) {
 #pragma unroll
-    for (int c2 = 0; c2 < CPT; ++c2)
-      if (CHUNKS % NT == 0 || tid + c2 * NT < CHUNKS) {
-        st16(smem + kb_ * L::KTILE + kdst[c2], pk[c2]);
-        st16(smem + vb_ * L::VTILE + vdst[c2], pv[c2]);
-      }
+    for (int c2 = 0; c2 < CPT; ++c2) {
+      st16(smem + kb_ * L::KTILE + kdst[c2], pk[c2]);
+      st16(smem + vb_ * L::VTILE + vdst[c2], pv[c2]);
+    }
+  };
+  auto refill = [&](int kb_, int vb_) {
+    lstore(kb_, vb_);
     __syncthreads();
   };
 
@@ -506,8 +517,62 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
         for (int u = 0; u < DT; ++u) acc[u][j] *= alpha[j];
     }
   };
+  // Unmasked steps: probabilities with the running max as it stands (no row max), summed with
+  // v_dot2 (fast_probs). A lane whose 16 probabilities sum above 2^12 (some score exceeds the
+  // max used in the exponent by more than 12 in base 2; an unset max gives +inf) sends the
+  // wave down the slow path (fast_fixup): row max, lazy update, accumulator rescale,
+  // probabilities recomputed. Probabilities fed to the MFMAs therefore stay at or below 2^12,
+  // far inside fp16, and rows whose max moves by less than that skip the max entirely.
+  auto fast_probs = [&](f32x16* scur, f16x8 (*pc)[2], float* ps) {
+    bool need = false;
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
+      const float nm = -mrow[j];
+      float acc_s = 0.0f;
+#pragma unroll
+      for (int sg = 0; sg < 2; ++sg) {
+        f16x8 x;
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          const float e0 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i], c, nm));
+          const float e1 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i + 1], c, nm));
+          const f16x2 pr = pack_f16(e0, e1);
+          acc_s = __builtin_amdgcn_fdot2(pr, ones, acc_s, false);
+          x[i] = pr[0];
+          x[i + 1] = pr[1];
+        }
+        pc[j][sg] = x;
+      }
+      ps[j] = acc_s;
+      need |= !(acc_s <= 4096.0f);
+    }
+    return need;
+  };
+  // kc_: K buffer still holding this step's keys: the slow path recomputes S from it, so S
+  // need not stay live through the fast path. The slow path is the body of a one-sided branch
+  // (the fast path's state updates come first and are undone there): a two-sided branch that
+  // updates the accumulators on one side only makes the register allocator double them.
+  auto fast_fixup = [&](bool need, f32x16* scur, f16x8 (*pc)[2], const float* ps, int kc_) {
+    float lprev[QT];
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
+      lprev[j] = lrow[j];
+      lrow[j] += ps[j];
+    }
+    if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+      for (int j = 0; j < QT; ++j) lrow[j] = lprev[j];
+      qk(scur, kc_);
+      float alpha[QT];
+      (void)softmax(scur, pc, alpha, 0, std::false_type{});
+#pragma unroll
+      for (int j = 0; j < QT; ++j)
+#pragma unroll
+        for (int u = 0; u < DT; ++u) acc[u][j] *= alpha[j];
+    }
+  };
 
-  // Prologue: K_0, K_1 into K buffers 0, 1; V_0 into V buffer 0; V buffer 3 (read by step 0
+  // Prologue: K_0, K_1 into K buffers 0, 1; V_0 into V buffer 0; V buffer 2 (read by step 0
   // together with all-zero probabilities) cleared.
   {
 #pragma unroll
@@ -524,7 +589,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
         st16(smem + kdst[c2], pk[c2]);
         st16(smem + L::KTILE + kdst[c2], k1[c2]);
         st16(smem + vdst[c2], pv[c2]);
-        st16(smem + 3 * L::VTILE + vdst[c2], u32x4{0, 0, 0, 0});
+        st16(smem + 2 * L::VTILE + vdst[c2], u32x4{0, 0, 0, 0});
       }
     __syncthreads();
   }
@@ -536,22 +601,26 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   if (wave_steps > 0) qk(sa, 0);
 
   // Steps before n_full need no mask for any wave of the workgroup (all keys below the
-  // workgroup's first query row and inside the sequence): they run branch-free, four per trip
-  // so buffer indices are constants and the S / P registers swap roles without copies. Loads
+  // workgroup's first query row and inside the sequence): they run six per trip so ring
+  // indices are constants and the S / P registers swap roles without copies. Loads
   // past the sequence end are harmless (zeros into a free buffer). Later steps mask per element
   // and let waves above their diagonal idle.
   const int n_full = CAUSAL ? min((qblk + 1) / 32, N / 32) : N / 32;
 
-  // Full step i with i % 4 == IV: PV of step i-1 (pprev), S of step i+1, softmax of step i.
+  // Full step i with i % 6 == IV: PV of step i-1 (pprev), S of step i+1, softmax of step i.
   auto full_step = [&](int i, f32x16* scur, f32x16* snext, const f16x8 (*pprev)[2], f16x8 (*pcur)[2],
                        auto iv_tag) {
     constexpr int IV = decltype(iv_tag)::value;
     gload(i);
-    pv_mma(pprev, (IV + 3) & 3);
-    qk(snext, (IV + 1) & 1);
-    float alpha[QT];
-    const bool upd = softmax(scur, pcur, alpha, 32 * i, std::false_type{});
-    // Interleave: loads first, then one MFMA for every few VALU instructions.
+    pv_mma(pprev, (IV + 2) % 3);
+    qk(snext, (IV + 1) % 3);
+    float ps[QT];
+    const bool need = fast_probs(scur, pcur, ps);
+    // The next tiles go to LDS before the slow path (their ring slots differ from the one it
+    // reads), which frees their registers for it; the stores still come last in the step so
+    // the global loads have the whole step to land.
+    lstore((IV + 2) % 3, (IV + 1) % 3);
+    // Interleave: loads first, then one MFMA for every few VALU instructions, stores last.
     __builtin_amdgcn_sched_group_barrier(0x020, 2 * CPT, 0);
 #pragma unroll
     for (int k2 = 0; k2 < 8 * QT; ++k2) {
@@ -559,28 +628,35 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
     }
-    rescale(upd, alpha);
-    refill(IV & 1, (IV + 1) & 3);
+    __builtin_amdgcn_sched_group_barrier(0x200, 2 * CPT, 0);
+    fast_fixup(need, scur, pcur, ps, IV % 3);
+    __syncthreads();
   };
 
   int i = 0;
-  for (; i + 3 < n_full; i += 4) {
+  for (; i + 5 < n_full; i += 6) {
     full_step(i, sa, sb, pa, pb, std::integral_constant<int, 0>{});
     full_step(i + 1, sb, sa, pb, pa, std::integral_constant<int, 1>{});
     full_step(i + 2, sa, sb, pa, pb, std::integral_constant<int, 2>{});
     full_step(i + 3, sb, sa, pb, pa, std::integral_constant<int, 3>{});
+    full_step(i + 4, sa, sb, pa, pb, std::integral_constant<int, 4>{});
+    full_step(i + 5, sb, sa, pb, pa, std::integral_constant<int, 5>{});
   }
   // Remaining steps (masked or not) with run-time buffer indices; state: scur = sa, pprev = pa.
   for (; i < nsteps; ++i) {
     gload(i);
-    if (i - 1 < wave_steps) pv_mma(pa, (i + 3) & 3);
+    if (i - 1 < wave_steps) pv_mma(pa, (i + 2) % 3);
     if (i < wave_steps) {
-      qk(sb, (i + 1) & 1);
+      qk(sb, (i + 1) % 3);
       float alpha[QT];
-      const bool mask = i >= n_full;
-      const bool upd = mask ? softmax(sa, pb, alpha, 32 * i, std::true_type{})
-                            : softmax(sa, pb, alpha, 32 * i, std::false_type{});
-      rescale(upd, alpha);
+      if (i >= n_full) {
+        const bool upd = softmax(sa, pb, alpha, 32 * i, std::true_type{});
+        rescale(upd, alpha);
+      } else {
+        float ps[QT];
+        const bool need = fast_probs(sa, pb, ps);
+        fast_fixup(need, sa, pb, ps, i % 3);
+      }
 #pragma unroll
       for (int j = 0; j < QT; ++j) {
         sa[j] = sb[j];
@@ -588,9 +664,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
         pa[j][1] = pb[j][1];
       }
     }
-    refill(i & 1, (i + 1) & 3);
+    refill((i + 2) % 3, (i + 1) % 3);
   }
-  if (wave_steps == nsteps && nsteps > 0) pv_mma(pa, (nsteps - 1) & 3);
+  if (wave_steps == nsteps && nsteps > 0) pv_mma(pa, (nsteps - 1) % 3);
 
 #pragma unroll
   for (int j = 0; j < QT; ++j) {

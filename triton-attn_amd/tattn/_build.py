@@ -19,6 +19,9 @@ REPO = PKG.parent.parent
 INCLUDE = REPO / "include"
 LIB = PKG / "libtattn_hip.so"
 SOURCES = ["abi.hip", "fwd.hip", "bwd.hip"]
+# Per-source flags. fwd.hip: keep each step's softmax work in the step that issues the
+# independent MFMAs it interleaves with (machine sinking would move it to its first use).
+SOURCE_FLAGS = {"fwd.hip": ["-mllvm", "-disable-machine-sink"]}
 ARCH = "gfx950"
 
 
@@ -54,7 +57,7 @@ def build(verbose: bool = False, extra: list[str] | None = None) -> Path:
     out.mkdir(exist_ok=True)
     objs = [out / (Path(s).stem + ".o") for s in SOURCES]
     with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        futs = [ex.submit(_compile, CSRC / s, o, extra) for s, o in zip(SOURCES, objs)]
+        futs = [ex.submit(_compile, CSRC / s, o, extra + SOURCE_FLAGS.get(s, [])) for s, o in zip(SOURCES, objs)]
         for f in futs:
             f.result()
     tmp = LIB.with_suffix(".so.tmp")

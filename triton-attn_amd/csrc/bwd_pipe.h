@@ -241,13 +241,6 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
     qk(snext, dnext, (st + 1) & 3);
     grad_mma(pprev, dsprev, (st + 3) & 3);
     pds(scur, dcur, pcur, dscur, st, lo + 32 * i, mask_tag);
-    __builtin_amdgcn_sched_group_barrier(0x020, 2 * CPT + 2, 0);
-#pragma unroll
-    for (int k2 = 0; k2 < 4 * NSD; ++k2) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-    }
     lstore((st + 2) & 3);
     __syncthreads();
   };
@@ -454,13 +447,6 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
     qk(snext, dnext, (st + 1) & 3);
     dq_mma(eprev, (st + 3) & 3);
     dsv(scur, dcur, ecur, 32 * i, std::false_type{});
-    __builtin_amdgcn_sched_group_barrier(0x020, 2 * CPT, 0);
-#pragma unroll
-    for (int k2 = 0; k2 < 2 * NSD + 2 * DT; ++k2) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-    }
     lstore((st + 2) & 3);
     __syncthreads();
   };

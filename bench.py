@@ -69,6 +69,22 @@ def _event_ms(fn, reps: int) -> float:
     return start.elapsed_time(end) / reps
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "fwd_pipe_traffic_fp16_d64_headline.md"
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per forward launch of the default headline workload, as measured with rocprofv3
+    FETCH_SIZE / WRITE_SIZE counters (calibrated on a plain copy) and recorded in TRAFFIC_FILE.
+    Counters cannot be read from inside the timed run, so the recorded figure is reported."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline() -> dict:
     """The oracle's tiled forward (restatement of the reference's CPU path) on the host CPU."""
     import torch
@@ -181,8 +197,11 @@ def main() -> int:
             fwd_flops += flops(data[n][0], HEADS, n, DIM, a.causal, "fwd")
     kernel_ms = sum(fwd_ms.values()) / len(seqs)  # average launch duration over the step
     achieved = fwd_flops / len(seqs) / (kernel_ms * 1e-3) / 1e12
+    traffic = None
+    if seqs == SEQS and not a.causal:
+        traffic = measured_traffic()
     roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
-                "frac": achieved / PEAK_F16_TFLOPS, "traffic": None,
+                "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic,
                 "kernel": f"tattn::fwd_pipe_kernel (fp16, D=64, {'causal' if a.causal else 'non-causal'})",
                 "avg_launch_ms": kernel_ms, "flops_per_launch": fwd_flops / len(seqs)}
 

@@ -7,10 +7,12 @@ Counted work follows the reference's benchmark (bench/bench.py:31-35 of amaanmit
 
 A timed step is one forward pass (non-causal, fp16) over each of the six 16,384-token shapes
 [B=16384/N, H=16, N, D=64] for N in 512..16384; inputs stay resident in HBM. `value` is the
-step's counted flops divided by its time. The same line carries the per-N sweep (forward, causal
-and non-causal; fwd+bwd, causal and non-causal, with peak extra memory), the roofline of the
-forward kernel (HIP-event kernel time on the launch stream) and a CPU baseline: the oracle's
-tiled forward timed on the host cores on a bounded sample.
+step's counted flops divided by its time. The same line carries the roofline of the forward
+kernel (HIP events around every forward launch of the timed steps, on the launch stream), the
+per-N sweep (forward, causal and non-causal; fwd+bwd, causal and non-causal, with peak extra
+memory) timed like the reference's tables (tattn.timing.do_bench: cache flushed before each
+call, median over ~100 ms), and a CPU baseline: the oracle's tiled forward timed on the host
+cores on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline]
 """
@@ -52,21 +54,6 @@ def _inputs(n: int, dev):
     q, k, v, do = (torch.randn(b, HEADS, n, DIM, device=dev, dtype=torch.float16, generator=g)
                    for _ in range(4))
     return b, q, k, v, do
-
-
-def _event_ms(fn, reps: int) -> float:
-    """Average ms per call of `fn` between two events on the current stream (the stream the
-    library launches on), after one untimed call."""
-    import torch
-
-    fn()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        fn()
-    end.record()
-    end.synchronize()
-    return start.elapsed_time(end) / reps
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "fwd_pipe_traffic_fp16_d64_headline.md"
@@ -119,7 +106,6 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--reps", type=int, default=10, help="calls per sweep cell")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="only the headline forward step")
     ap.add_argument("--seqs", default=",".join(map(str, SEQS)),
@@ -139,6 +125,7 @@ def main() -> int:
 
     from tattn import attention, hip_available
     from tattn.api import _forward
+    from tattn.timing import do_bench
 
     dev = torch.device("cuda:0")
     if not hip_available(dev):
@@ -164,13 +151,23 @@ def main() -> int:
             _, q, k, v, _ = data[n]
             grads[n] = tuple(t.detach().clone().requires_grad_() for t in (q, k, v))
 
-    def step() -> None:
+    # Forward mode: every launch of the timed steps is bracketed by events on the launch stream;
+    # their durations give the roofline's average launch time over the timed region.
+    launch_events: list[tuple[int, object, object]] = []
+
+    def step(record: bool = False) -> None:
         for n in seqs:
             _, q, k, v, do = data[n]
             if a.backward:
                 qg, kg, vg = grads[n]
                 qg.grad = kg.grad = vg.grad = None
                 attention(qg, kg, vg, causal=a.causal).backward(do)
+            elif record:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                _forward(q, k, v, a.causal, scale)
+                e1.record()
+                launch_events.append((n, e0, e1))
             else:
                 _forward(q, k, v, a.causal, scale)
 
@@ -181,29 +178,36 @@ def main() -> int:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(a.steps):
-            step()
+            step(record=True)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / a.steps
     value = step_flops / (ms_per_step * 1e-3) / 1e12
 
-    # ---- roofline of the forward kernel: event-timed launches of each shape -------------
-    fwd_ms = {}
-    fwd_flops = 0.0
-    with torch.inference_mode():
-        for n in seqs:
-            _, q, k, v, _ = data[n]
-            fwd_ms[n] = _event_ms(lambda: _forward(q, k, v, a.causal, scale), a.reps)
-            fwd_flops += flops(data[n][0], HEADS, n, DIM, a.causal, "fwd")
-    kernel_ms = sum(fwd_ms.values()) / len(seqs)  # average launch duration over the step
-    achieved = fwd_flops / len(seqs) / (kernel_ms * 1e-3) / 1e12
+    # ---- roofline of the forward kernel over the timed region ----------------------------
+    if not launch_events:  # fwd+bwd headline: time the forward launches of the same shapes
+        with torch.inference_mode():
+            for _ in range(a.steps):
+                for n in seqs:
+                    _, q, k, v, _ = data[n]
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    _forward(q, k, v, a.causal, scale)
+                    e1.record()
+                    launch_events.append((n, e0, e1))
+        torch.cuda.synchronize()
+    durations = [e0.elapsed_time(e1) for _, e0, e1 in launch_events]
+    fwd_flops = sum(flops(data[n][0], HEADS, n, DIM, a.causal, "fwd") for n, _, _ in launch_events)
+    kernel_ms = sum(durations) / len(durations)  # average launch duration
+    achieved = fwd_flops / len(durations) / (kernel_ms * 1e-3) / 1e12
     traffic = None
     if seqs == SEQS and not a.causal:
         traffic = measured_traffic()
     roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                 "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic,
                 "kernel": f"tattn::fwd_pipe_kernel (fp16, D=64, {'causal' if a.causal else 'non-causal'})",
-                "avg_launch_ms": kernel_ms, "flops_per_launch": fwd_flops / len(seqs)}
+                "avg_launch_ms": kernel_ms, "launches": len(durations),
+                "flops_per_launch": fwd_flops / len(durations)}
 
     # ---- sweep: per N, forward and fwd+bwd, causal and non-causal -------------------------
     sweep = []
@@ -216,7 +220,7 @@ def main() -> int:
                     b, q, k, v, do = data[n]
                     if mode == "fwd":
                         with torch.inference_mode():
-                            ms = _event_ms(lambda: attention(q, k, v, causal=causal), a.reps)
+                            ms = do_bench(lambda: attention(q, k, v, causal=causal))
                         peak_mib = None
                     else:
                         qg, kg, vg = (t.detach().clone().requires_grad_() for t in (q, k, v))
@@ -233,7 +237,7 @@ def main() -> int:
                         fb()
                         torch.cuda.synchronize()
                         peak_mib = (torch.cuda.max_memory_allocated() - base) / 2**20
-                        ms = _event_ms(fb, a.reps)
+                        ms = do_bench(fb)
                         del qg, kg, vg
                     f = flops(b, HEADS, n, DIM, causal, mode)
                     tf = f / (ms * 1e-3) / 1e12

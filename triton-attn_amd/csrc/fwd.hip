@@ -309,25 +309,29 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_generic_kernel(const FwdParams
 // per-lane sum check sends the wave to a slow path (row max, rescale, S recomputed from the
 // K tile still in LDS) only when some probability could exceed 2^12, which after the first
 // step is rare. Masked steps (diagonal, sequence end) always take the full softmax.
-// LDS rings of three tiles each: step i reads K_{i+1} (and K_i on the slow path) and V_{i-1},
-// and refills K[(i+2)%3] with K_{i+2} and V[(i+1)%3] with V_{i+1}; one barrier per step.
-// Tiles are read from HBM with range-checked buffer loads: rows past the sequence end come
-// back as zeros.
+// LDS rings of four tiles each, filled by LDS DMA (range-checked buffer loads that write LDS
+// directly, no registers): step i reads K_{i+1} (and K_i on the slow path) and V_{i-1}, and
+// starts K_{i+3} and V_{i+1}, which have two steps to arrive; one barrier per step. Rows past
+// the sequence end come back as zeros.
 // LDS row strides: K rows D*2+16 bytes (16 consecutive rows of a 16-byte column hit distinct
 // banks); V rows are an odd multiple of 64 bytes so each transposed read (4 rows x 64 bytes per
 // 32 lanes) covers distinct banks of gfx950's 64-bank LDS.
 
 template <int D>
 struct PipeLayout {
-  static constexpr int RK = D * 2 + 16;
+  static constexpr int RK = D * 2 + 16;  // LDS row bytes of K and V tiles
   static constexpr int RV = D == 16 ? 64 : D == 32 ? 64 : D == 64 ? 192 : 320;
-  static constexpr int KTILE = 32 * RK;
-  static constexpr int VTILE = 32 * RV;
-  // Three-deep rings: during step i the kernel reads K_{i+1} (S of the next step) and, on the
-  // rare slow softmax path, K_i, and reads V_{i-1}; it writes K_{i+2} and V_{i+1}.
-  static constexpr int NKBUF = 3, NVBUF = 3;
-  static constexpr int VBASE = NKBUF * KTILE;
-  static constexpr int LDS = VBASE + NVBUF * VTILE;
+  // Tiles arrive by LDS DMA (buffer_load ... lds): one wave instruction writes 64 lanes x 16
+  // bytes to 1 KB of consecutive LDS, so a slot holds whole 1 KB pieces; lanes that land on row
+  // padding or past the 32 rows fetch a duplicate chunk into that slack.
+  static constexpr int KPIECES = (32 * RK / 16 + 63) / 64;
+  static constexpr int VPIECES = (32 * RV / 16 + 63) / 64;
+  static constexpr int KSLOT = 1024 * KPIECES, VSLOT = 1024 * VPIECES;
+  // Four-deep rings: during step i the kernel reads K_{i+1} (S of the next step), K_i (rare
+  // slow softmax path) and V_{i-1}, while K_{i+2} and V_i sit landed and K_{i+3}, V_{i+1} are in
+  // flight (issued at the start of step i, needed two steps later).
+  static constexpr int NSLOT = 4;
+  static constexpr int LDS = NSLOT * (KSLOT + VSLOT);
 };
 
 template <int D, int NW, int QT, int OCC, bool CAUSAL>
@@ -336,10 +340,16 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   constexpr int NT = NW * 64, BM = NW * QT * 32;
   constexpr int NSD = D / 16;        // 16-wide d slices of S = K Q^T
   constexpr int DT = (D + 31) / 32;  // 32-row d tiles of O^T
-  constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
-  constexpr int CHUNKS = 32 * CPR;
-  constexpr int CPT = (CHUNKS + NT - 1) / NT;
-  __shared__ __attribute__((aligned(16))) char smem[L::LDS];
+  constexpr int CPK = (L::KPIECES + NW - 1) / NW;  // K and V DMA instructions per wave per step
+  constexpr int CPV = (L::VPIECES + NW - 1) / NW;
+  constexpr int CPW = CPK + CPV;
+  static_assert(CPW < 16, "vmcnt field");
+  // One array per ring slot: distinct objects let the compiler see that a DMA into one slot
+  // does not alias reads of another (no conservative waits on in-flight tiles).
+  __shared__ __attribute__((aligned(1024))) char ks0[L::KSLOT], ks1[L::KSLOT], ks2[L::KSLOT], ks3[L::KSLOT];
+  __shared__ __attribute__((aligned(1024))) char vs0[L::VSLOT], vs1[L::VSLOT], vs2[L::VSLOT], vs3[L::VSLOT];
+  auto kbuf = [&](int s) -> char* { return s == 0 ? ks0 : s == 1 ? ks1 : s == 2 ? ks2 : ks3; };
+  auto vbuf = [&](int s) -> char* { return s == 0 ? vs0 : s == 1 ? vs1 : s == 2 ? vs2 : vs3; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6, h2 = lane >> 5, l32 = lane & 31;
@@ -378,46 +388,55 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   // Steps this wave computes: every step up to the one holding its last query row.
   const int wave_steps = qw0 >= N ? 0 : CAUSAL ? min(nsteps, (qw0 + 32 * QT - 1) / 32 + 1) : nsteps;
 
-  // This thread's chunks of a 32-row tile: byte offsets in HBM (from the step's first row) and
-  // in the LDS tile. Per-lane LDS operand addresses are fixed too; tiles differ by constants.
-  uint32_t koff[CPT], voff[CPT];
-  int kdst[CPT], vdst[CPT];
+  // DMA work of this wave: pieces w, w + NW, ... of the step's K tile and of its V tile (indices
+  // past a tile's last piece wrap around: a duplicate piece writes the same bytes again). For
+  // each, the lane's HBM byte offset from the tile's first row: LDS chunk j = 64 * piece + lane
+  // of the padded tile holds row j / (R / 16), chunk j % (R / 16); K rows are in perm32 order.
+  const int wu = (int)uniform32((uint32_t)w);
+  int kpc[CPK], vpc[CPV];
+  uint32_t kgo[CPK], vgo[CPV];
+  auto piece = [&](int pp, int rb, int64_t rstride, bool perm, uint32_t& go) {
+    const int cpr = rb / 16;
+    const int j = 64 * pp + lane;
+    const int row = min(j / cpr, 31);
+    const int cc = min(j % cpr, D / 8 - 1);
+    go = (uint32_t)((perm ? perm32(row) : row) * rstride * 2 + cc * 16);
+  };
 #pragma unroll
-  for (int i = 0; i < CPT; ++i) {
-    const int ch = min(tid + i * NT, CHUNKS - 1);
-    const int row = ch / CPR, cb = (ch % CPR) * 16;
-    koff[i] = (uint32_t)(row * p.sk[2] * 2 + cb);
-    voff[i] = (uint32_t)(row * p.sv[2] * 2 + cb);
-    kdst[i] = perm32(row) * L::RK + cb;
-    vdst[i] = L::VBASE + row * L::RV + cb;
+  for (int t = 0; t < CPK; ++t) {
+    const int pp = (wu + NW * t) % L::KPIECES;
+    kpc[t] = 1024 * pp;
+    piece(pp, L::RK, p.sk[2], true, kgo[t]);
   }
+#pragma unroll
+  for (int t = 0; t < CPV; ++t) {
+    const int pp = (wu + NW * t) % L::VPIECES;
+    vpc[t] = 1024 * pp;
+    piece(pp, L::RV, p.sv[2], false, vgo[t]);
+  }
+  // K tile kt into K slot ks, V tile vt into V slot vs (tiles past the sequence read as zero).
+  auto dma = [&](int kt, int vt, int ks, int vs) {
+#pragma unroll
+    for (int t = 0; t < CPK; ++t)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (TATTN_LDS void*)(kbuf(ks) + kpc[t]), 16,
+                                               (int)(kgo[t] + (uint32_t)kt * k_step), 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < CPV; ++t)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (TATTN_LDS void*)(vbuf(vs) + vpc[t]), 16,
+                                               (int)(vgo[t] + (uint32_t)vt * v_step), 0, 0, 0);
+  };
+  // End of a step: this wave's DMAs of the previous step have landed and its LDS reads are done
+  // (this step's DMAs stay in flight), then the barrier publishes the landed tiles. The signal
+  // fences keep the compiler from moving LDS reads across the barrier.
+  auto step_end = [&]() {
+    __builtin_amdgcn_s_waitcnt(0x0070 | CPW);  // vmcnt(CPW), lgkmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
   const int g = lane >> 4, src = lane & 15;
   const int kop_off = l32 * L::RK + 16 * h2;
-  const int vop_off = L::VBASE + (8 * (g >> 1) + (src >> 2)) * L::RV + (16 * (g & 1) + 4 * (src & 3)) * 2;
-
-  u32x4 pk[CPT], pv[CPT];
-  auto gload = [&](int i) {  // K_{i+2}, V_{i+1}
-#pragma unroll
-    for (int c2 = 0; c2 < CPT; ++c2) {
-      pk[c2] = rsrc_load(krs, koff[c2] + (uint32_t)(i + 2) * k_step);
-      pv[c2] = rsrc_load(vrs, voff[c2] + (uint32_t)(i + 1) * v_step);
-    }
-  };
-  // kb_: K buffer of K_{i+2} (== (i + 2) % 3); vb_: V buffer of V_{i+1} (== (i + 1) % 3)
-  // Unguarded: a thread past the last chunk has its chunk index clamped to the last one, so it
-  // stores the same bytes to the same address as that chunk's owner (a branch here would split
-  // the step's scheduling region).
-  auto lstore = [&](int kb_, int vb_) {
-#pragma unroll
-    for (int c2 = 0; c2 < CPT; ++c2) {
-      st16(smem + kb_ * L::KTILE + kdst[c2], pk[c2]);
-      st16(smem + vb_ * L::VTILE + vdst[c2], pv[c2]);
-    }
-  };
-  auto refill = [&](int kb_, int vb_) {
-    lstore(kb_, vb_);
-    __syncthreads();
-  };
+  const int vop_off = (8 * (g >> 1) + (src >> 2)) * L::RV + (16 * (g & 1) + 4 * (src & 3)) * 2;
 
   // S = K Q^T for the 32-key tile in K buffer kb_ (C layout: lane = query, register r = key
   // kappa(r, h2)).
@@ -426,8 +445,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
     for (int j = 0; j < QT; ++j) s[j] = f32x16{};
 #pragma unroll
     for (int sd = 0; sd < NSD; ++sd) {
-      const f16x8 kop =
-          *reinterpret_cast<const TATTN_LDS f16x8*>((const TATTN_LDS char*)smem + kb_ * L::KTILE + kop_off + 32 * sd);
+      const f16x8 kop = *reinterpret_cast<const TATTN_LDS f16x8*>((const TATTN_LDS char*)kbuf(kb_) + kop_off + 32 * sd);
 #pragma unroll
       for (int j = 0; j < QT; ++j) s[j] = Elt<f16>::mfma(kop, qop[j][sd], s[j]);
     }
@@ -450,8 +468,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
     for (int u = 0; u < DT; ++u) {
 #pragma unroll
       for (int sg = 0; sg < 2; ++sg) {
-        const TATTN_LDS char* a =
-            (const TATTN_LDS char*)smem + vb_ * L::VTILE + vop_off + 16 * sg * L::RV + 64 * u;
+        const TATTN_LDS char* a = (const TATTN_LDS char*)vbuf(vb_) + vop_off + 16 * sg * L::RV + 64 * u;
         const f16x4 lo = lds_read_tr(a), hi4 = lds_read_tr(a + 4 * L::RV);
         f16x8 vop = f16x8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
         if (D < 32 && 32 * u + 16 * (g & 1) >= D) vop = f16x8{};
@@ -572,27 +589,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
     }
   };
 
-  // Prologue: K_0, K_1 into K buffers 0, 1; V_0 into V buffer 0; V buffer 2 (read by step 0
-  // together with all-zero probabilities) cleared.
-  {
-#pragma unroll
-    for (int c2 = 0; c2 < CPT; ++c2) {
-      pk[c2] = rsrc_load(krs, koff[c2]);
-      pv[c2] = rsrc_load(vrs, voff[c2]);
-    }
-    u32x4 k1[CPT];
-#pragma unroll
-    for (int c2 = 0; c2 < CPT; ++c2) k1[c2] = rsrc_load(krs, koff[c2] + k_step);
-#pragma unroll
-    for (int c2 = 0; c2 < CPT; ++c2)
-      if (CHUNKS % NT == 0 || tid + c2 * NT < CHUNKS) {
-        st16(smem + kdst[c2], pk[c2]);
-        st16(smem + L::KTILE + kdst[c2], k1[c2]);
-        st16(smem + vdst[c2], pv[c2]);
-        st16(smem + 2 * L::VTILE + vdst[c2], u32x4{0, 0, 0, 0});
-      }
-    __syncthreads();
-  }
+  // Prologue: K_0..K_2 and V_0..V_2 into slots 0..2; V slot 3 (read by step 0 together with
+  // all-zero probabilities) cleared.
+  dma(0, 0, 0, 0);
+  dma(1, 1, 1, 1);
+  dma(2, 2, 2, 2);
+  for (int o = tid * 16; o < L::VSLOT; o += NT * 16) st16(vs3 + o, u32x4{0, 0, 0, 0});
+  __syncthreads();
 
   f32x16 sa[QT], sb[QT];
   f16x8 pa[QT][2], pb[QT][2];
@@ -601,44 +604,41 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   if (wave_steps > 0) qk(sa, 0);
 
   // Steps before n_full need no mask for any wave of the workgroup (all keys below the
-  // workgroup's first query row and inside the sequence): they run six per trip so ring
-  // indices are constants and the S / P registers swap roles without copies. Loads
-  // past the sequence end are harmless (zeros into a free buffer). Later steps mask per element
-  // and let waves above their diagonal idle.
+  // workgroup's first query row and inside the sequence): they run four per trip so ring
+  // slots are constants and the S / P registers swap roles without copies. Tiles fetched past
+  // the sequence end are harmless (zeros into a free slot). Later steps mask per element and
+  // let waves above their diagonal idle.
   const int n_full = CAUSAL ? min((qblk + 1) / 32, N / 32) : N / 32;
 
-  // Full step i with i % 6 == IV: PV of step i-1 (pprev), S of step i+1, softmax of step i.
+  // Full step i with i % 4 == IV: PV of step i-1 (pprev), S of step i+1, softmax of step i;
+  // K_{i+3} and V_{i+1} start streaming into the slots freed two steps ago. The instruction
+  // order within the step is left to the compiler (measured faster than pinned MFMA/VALU
+  // interleave patterns).
   auto full_step = [&](int i, f32x16* scur, f32x16* snext, const f16x8 (*pprev)[2], f16x8 (*pcur)[2],
                        auto iv_tag) {
     constexpr int IV = decltype(iv_tag)::value;
-    gload(i);
-    pv_mma(pprev, (IV + 2) % 3);
-    qk(snext, (IV + 1) % 3);
+    dma(i + 3, i + 1, (IV + 3) % 4, (IV + 1) % 4);
+    pv_mma(pprev, (IV + 3) % 4);
+    qk(snext, (IV + 1) % 4);
     float ps[QT];
     const bool need = fast_probs(scur, pcur, ps);
-    // The next tiles go to LDS before the slow path (their ring slots differ from the one it
-    // reads), which frees their registers for it. The instruction order within the step is
-    // left to the compiler: measured faster than pinned MFMA/VALU interleave patterns.
-    lstore((IV + 2) % 3, (IV + 1) % 3);
-    fast_fixup(need, scur, pcur, ps, IV % 3);
-    __syncthreads();
+    fast_fixup(need, scur, pcur, ps, IV);
+    step_end();
   };
 
   int i = 0;
-  for (; i + 5 < n_full; i += 6) {
+  for (; i + 3 < n_full; i += 4) {
     full_step(i, sa, sb, pa, pb, std::integral_constant<int, 0>{});
     full_step(i + 1, sb, sa, pb, pa, std::integral_constant<int, 1>{});
     full_step(i + 2, sa, sb, pa, pb, std::integral_constant<int, 2>{});
     full_step(i + 3, sb, sa, pb, pa, std::integral_constant<int, 3>{});
-    full_step(i + 4, sa, sb, pa, pb, std::integral_constant<int, 4>{});
-    full_step(i + 5, sb, sa, pb, pa, std::integral_constant<int, 5>{});
   }
-  // Remaining steps (masked or not) with run-time buffer indices; state: scur = sa, pprev = pa.
+  // Remaining steps (masked or not) with run-time slots; state: scur = sa, pprev = pa.
   for (; i < nsteps; ++i) {
-    gload(i);
-    if (i - 1 < wave_steps) pv_mma(pa, (i + 2) % 3);
+    dma(i + 3, i + 1, (i + 3) & 3, (i + 1) & 3);
+    if (i - 1 < wave_steps) pv_mma(pa, (i + 3) & 3);
     if (i < wave_steps) {
-      qk(sb, (i + 1) % 3);
+      qk(sb, (i + 1) & 3);
       float alpha[QT];
       if (i >= n_full) {
         const bool upd = softmax(sa, pb, alpha, 32 * i, std::true_type{});
@@ -646,7 +646,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
       } else {
         float ps[QT];
         const bool need = fast_probs(sa, pb, ps);
-        fast_fixup(need, sa, pb, ps, i % 3);
+        fast_fixup(need, sa, pb, ps, i & 3);
       }
 #pragma unroll
       for (int j = 0; j < QT; ++j) {
@@ -655,9 +655,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
         pa[j][1] = pb[j][1];
       }
     }
-    refill((i + 2) % 3, (i + 1) % 3);
+    step_end();
   }
-  if (wave_steps == nsteps && nsteps > 0) pv_mma(pa, (nsteps - 1) % 3);
+  if (wave_steps == nsteps && nsteps > 0) pv_mma(pa, (nsteps - 1) & 3);
+  // No LDS DMA may still be in flight when the workgroup's LDS is released.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
 #pragma unroll
   for (int j = 0; j < QT; ++j) {

@@ -61,7 +61,8 @@ int tattn_device_supported(void);
  * Forward: o = softmax(q k^T * sm_scale [causal mask]) v, m = per-row base-2 log-sum-exp.
  * Replaces `_forward` + `_fwd_kernel` of the reference
  * (src/tattn/api.py:78-99, src/tattn/kernels.py:57-148). Arbitrary z/h/n strides per tensor
- * (api.py:95-96); m is [Z,H,N] float32 contiguous (api.py:88).
+ * (api.py:95-96); m is [Z,H,N] float32 contiguous (api.py:88), or NULL when no backward will
+ * follow: the log-sum-exp is then not stored (the reference always stores it, api.py:88, 161).
  * config_id = -1 picks from the table by (D, dtype, causal, N); otherwise an index into
  * the TATTN_K_FWD table (the reference's `config=` override, api.py:69-75).
  */

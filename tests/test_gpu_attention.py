@@ -228,3 +228,24 @@ def test_one_hip_runtime_mapped():
     paths = {line.split()[-1] for line in maps if "libamdhip64" in line}
     assert len(paths) == 1, paths
     assert any("libtattn_hip.so" in line for line in maps)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_inference_path_matches_autograd_path(causal, dtype):
+    """Without grad, attention keeps no autograd state and stores no log-sum-exp (tattn_fwd with
+    m = NULL); its output is bitwise the autograd path's."""
+    from tattn import attention
+    from tattn.api import _forward
+
+    q, k, v = (r((2, 3, 300, 64), dtype, s) for s in (100, 101, 102))
+    qg = q.clone().requires_grad_()
+    o_grad = attention(qg, k, v, causal=causal)
+    with torch.no_grad():
+        o_nograd = attention(qg, k, v, causal=causal)
+    o_plain = attention(q, k, v, causal=causal)  # no input requires grad
+    assert o_grad.grad_fn is not None and o_nograd.grad_fn is None and o_plain.grad_fn is None
+    assert torch.equal(o_nograd, o_grad.detach()) and torch.equal(o_plain, o_grad.detach())
+    o2, m2 = _forward(q, k, v, causal, 0.125, save_lse=False)
+    o3, m3 = _forward(q, k, v, causal, 0.125)
+    assert m2 is None and m3 is not None and torch.equal(o2, o3)

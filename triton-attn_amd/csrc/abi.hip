@@ -199,7 +199,7 @@ int tattn_fwd(const void* q, const void* k, const void* v, void* o, float* m, co
   if ((rc = check_tensor("q", q, q_strides, sz)) || (rc = check_tensor("k", k, k_strides, sz)) ||
       (rc = check_tensor("v", v, v_strides, sz)) || (rc = check_tensor("o", o, o_strides, sz)))
     return rc;
-  if (!m) return set_error(TATTN_E_ARG, "m is a null pointer");
+  // m may be null: the log-sum-exp is then not stored (no backward will follow).
   int id;
   if ((rc = resolve(TATTN_K_FWD, D, dtype, causal, N, config_id, &id))) return rc;
   if ((rc = device_check())) return rc;

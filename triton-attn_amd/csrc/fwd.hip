@@ -72,7 +72,7 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_generic_kernel(const FwdParams
   const T* K = (const T*)p.k + z * p.sk[0] + hh * p.sk[1];
   const T* V = (const T*)p.v + z * p.sv[0] + hh * p.sv[1];
   T* O = (T*)p.o + z * p.so[0] + hh * p.so[1];
-  float* M = p.m + (int64_t)zh * N;
+  float* M = p.m ? p.m + (int64_t)zh * N : nullptr;  // null: M not stored
   const int64_t sqn = p.sq[2], skn = p.sk[2], svn = p.sv[2], son = p.so[2];
   const float c = p.c;
 
@@ -295,7 +295,7 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_generic_kernel(const FwdParams
             }
           }
         }
-      if (h2 == 0) M[q] = mrow[j] + __log2f(lt);
+      if (h2 == 0 && M) M[q] = mrow[j] + __log2f(lt);
     }
   }
 }
@@ -361,7 +361,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   const int64_t z = zh / p.H, hh = zh % p.H;
   const f16* Q = (const f16*)p.q + z * p.sq[0] + hh * p.sq[1];
   f16* O = (f16*)p.o + z * p.so[0] + hh * p.so[1];
-  float* M = p.m + (int64_t)zh * N;
+  float* M = p.m ? p.m + (int64_t)zh * N : nullptr;  // null: M not stored
   const int64_t sqn = p.sq[2], son = p.so[2];
   const __amdgpu_buffer_rsrc_t krs = slice_rsrc((const f16*)p.k + z * p.sk[0] + hh * p.sk[1], slice_bytes(N, p.sk[2], D));
   const __amdgpu_buffer_rsrc_t vrs = slice_rsrc((const f16*)p.v + z * p.sv[0] + hh * p.sv[1], slice_bytes(N, p.sv[2], D));
@@ -680,7 +680,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
             *reinterpret_cast<f16x4*>(orow + d0) = x;
           }
         }
-      if (h2 == 0) M[q] = mrow[j] + __log2f(lt);
+      if (h2 == 0 && M) M[q] = mrow[j] + __log2f(lt);
     }
   }
 }

@@ -111,19 +111,20 @@ def _stream(t: torch.Tensor) -> int:
 
 def _forward(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: float,
-    config: Config = None,
-) -> tuple[torch.Tensor, torch.Tensor]:
-    """(O, M): O in q's layout, M = [Z, H, N] float32 base-2 log-sum-exp (api.py:78-99)."""
+    config: Config = None, *, save_lse: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """(O, M): O in q's layout, M = [Z, H, N] float32 base-2 log-sum-exp (api.py:78-99).
+    save_lse=False (no backward will follow) skips M: neither allocated nor stored, M is None."""
     _require_gpu(q)
     lib = _lib.load()
     q, k, v = (_kernel_layout(t) for t in (q, k, v))
     z, h, n, d = q.shape
     o = torch.empty_like(q)
-    m = torch.empty((z, h, n), device=q.device, dtype=torch.float32)
+    m = torch.empty((z, h, n), device=q.device, dtype=torch.float32) if save_lse else None
     cid = _resolve(_lib.K_FWD, d, q.dtype, config, causal, n)
     with torch.cuda.device(q.device):
         rc = lib.tattn_fwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), m.data_ptr(),
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), m.data_ptr() if m is not None else None,
             _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(o),
             z, h, n, d, _DTYPES[q.dtype], int(causal), float(scale), cid, _stream(q),
         )
@@ -193,6 +194,10 @@ def attention(
     softmax(q k^T * sm_scale [causal: key <= query]) v, sm_scale defaulting to 1/sqrt(dim)."""
     _check(q, k, v)
     scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    if not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)):
+        # Inference: no autograd context and no log-sum-exp to save (the reference always saves
+        # both, api.py:161); the output is the same.
+        return _forward(q, k, v, causal, scale, save_lse=False)[0]
     out: torch.Tensor = _Attention.apply(q, k, v, causal, scale)
     return out
 

@@ -6,7 +6,7 @@
  * The caller owns every buffer (outputs and the float32 M / delta workspaces).
  *
  * Layouts. q, k, v, o, do, dq, dk, dv are [Z, H, N, D] tensors of one element type
- * (TATTN_F16 or TATTN_F32). Strides are in ELEMENTS, four per tensor, ordered
+ * (TATTN_F16, TATTN_BF16 or TATTN_F32). Strides are in ELEMENTS, four per tensor, ordered
  * (z, h, n, d). The d stride must be 1, rows must be 16-byte aligned. M and delta are
  * float32 [Z, H, N], contiguous. Head dims: 16, 32, 64, 128.
  *
@@ -28,7 +28,9 @@ extern "C" {
 
 #define TATTN_ABI_VERSION 1
 
-enum tattn_dtype { TATTN_F16 = 0, TATTN_F32 = 1 };
+/* TATTN_BF16 has no counterpart in the reference, which accepts fp16 and fp32 only
+ * (src/tattn/api.py:55-56); it runs the fp16 kernels with bf16 MFMAs and bf16 rounding points. */
+enum tattn_dtype { TATTN_F16 = 0, TATTN_F32 = 1, TATTN_BF16 = 2 };
 enum tattn_kernel { TATTN_K_FWD = 0, TATTN_K_BWD_DKDV = 1, TATTN_K_BWD_DQ = 2 };
 enum tattn_status {
   TATTN_OK = 0,

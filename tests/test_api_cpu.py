@@ -30,12 +30,18 @@ def test_rejects_mixed_devices():
         attention(x, x.to("meta"), x)
 
 
-def test_rejects_bfloat16_and_mixed_dtypes():
+def test_rejects_mixed_and_unsupported_dtypes():
+    """tests/test_attention.py:74-75; bfloat16 is accepted (an addition to the reference),
+    float64 and mixed dtypes are not."""
     x = torch.zeros(1, 1, 8, 16)
     with pytest.raises(ValueError, match="dtype"):
-        attention(x.bfloat16(), x.bfloat16(), x.bfloat16())
-    with pytest.raises(ValueError, match="dtype"):
         attention(x.half(), x, x)
+    with pytest.raises(ValueError, match="dtype"):
+        attention(x.double(), x.double(), x.double())
+    with pytest.raises(ValueError, match="dtype"):
+        attention(x.bfloat16(), x.half(), x.bfloat16())
+    with pytest.raises(RuntimeError, match="gfx950"):  # valid, but CPU tensors have no path
+        attention(x.bfloat16(), x.bfloat16(), x.bfloat16())
 
 
 def test_cpu_tensors_are_refused_not_computed():

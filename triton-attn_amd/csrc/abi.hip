@@ -76,8 +76,9 @@ const TileEntry* table_entry(int64_t D, int id) {
   return id >= 0 && id < n ? e + id : nullptr;
 }
 
+// fp16 and bf16 share the 16-bit tables (tiles.h).
 int num_configs(int kernel, int64_t D, int dtype) {
-  const bool h = dtype == TATTN_F16;
+  const bool h = dtype != TATTN_F32;
   switch (kernel) {
     case TATTN_K_FWD: return h ? table_size<FwdTable, _Float16>(D) : table_size<FwdTable, float>(D);
     case TATTN_K_BWD_DKDV: return h ? table_size<DkdvTable, _Float16>(D) : table_size<DkdvTable, float>(D);
@@ -87,7 +88,7 @@ int num_configs(int kernel, int64_t D, int dtype) {
 }
 
 const TileEntry* config_entry(int kernel, int64_t D, int dtype, int id) {
-  const bool h = dtype == TATTN_F16;
+  const bool h = dtype != TATTN_F32;
   switch (kernel) {
     case TATTN_K_FWD: return h ? table_entry<FwdTable, _Float16>(D, id) : table_entry<FwdTable, float>(D, id);
     case TATTN_K_BWD_DKDV:
@@ -102,7 +103,7 @@ const TileEntry* config_entry(int kernel, int64_t D, int dtype, int id) {
 // below are the fastest entries measured on an MI355X at 16,384 tokens per batch, H=16. Entry 0
 // of each table is its general-purpose tile.
 int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N) {
-  if (dtype != TATTN_F16 || D != 64) return 0;
+  if (dtype == TATTN_F32 || D != 64) return 0;  // fp16 and bf16 share the picks
   switch (kernel) {
     case TATTN_K_FWD:  // short rows: 128-row blocks; long: 256 rows (causal) or 512 rows
       if (causal) return N >= 8192 ? 0 : 1;
@@ -130,8 +131,8 @@ int check_tensor(const char* name, const void* ptr, const int64_t* st, int sz) {
 }
 
 int check_shape(int64_t Z, int64_t H, int64_t N, int64_t D, int dtype) {
-  if (dtype != TATTN_F16 && dtype != TATTN_F32)
-    return set_error(TATTN_E_ARG, "dtype must be TATTN_F16 or TATTN_F32, got %d", dtype);
+  if (dtype != TATTN_F16 && dtype != TATTN_F32 && dtype != TATTN_BF16)
+    return set_error(TATTN_E_ARG, "dtype must be TATTN_F16, TATTN_BF16 or TATTN_F32, got %d", dtype);
   if (D != 16 && D != 32 && D != 64 && D != 128)
     return set_error(TATTN_E_ARG, "head dim must be 16, 32, 64 or 128, got %lld", (long long)D);
   if (Z < 1 || H < 1 || N < 1) return set_error(TATTN_E_ARG, "Z, H, N must be positive (%lld, %lld, %lld)",
@@ -195,7 +196,7 @@ int tattn_fwd(const void* q, const void* k, const void* v, void* o, float* m, co
               void* stream) {
   int rc;
   if ((rc = check_shape(Z, H, N, D, dtype))) return rc;
-  const int sz = dtype == TATTN_F16 ? 2 : 4;
+  const int sz = dtype == TATTN_F32 ? 4 : 2;
   if ((rc = check_tensor("q", q, q_strides, sz)) || (rc = check_tensor("k", k, k_strides, sz)) ||
       (rc = check_tensor("v", v, v_strides, sz)) || (rc = check_tensor("o", o, o_strides, sz)))
     return rc;
@@ -230,7 +231,7 @@ int tattn_bwd_preprocess(const void* o, const void* dout, float* delta, const in
   BwdParams p{};
   int rc;
   if ((rc = bwd_common(p, strides, Z, H, N, D, dtype, 1.0f))) return rc;
-  const int sz = dtype == TATTN_F16 ? 2 : 4;
+  const int sz = dtype == TATTN_F32 ? 4 : 2;
   if ((rc = check_tensor("o", o, strides, sz)) || (rc = check_tensor("do", dout, strides, sz))) return rc;
   if (!delta) return set_error(TATTN_E_ARG, "delta is a null pointer");
   if ((rc = device_check())) return rc;
@@ -244,7 +245,7 @@ int tattn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout
   BwdParams p{};
   int rc;
   if ((rc = bwd_common(p, strides, Z, H, N, D, dtype, sm_scale))) return rc;
-  const int sz = dtype == TATTN_F16 ? 2 : 4;
+  const int sz = dtype == TATTN_F32 ? 4 : 2;
   if ((rc = check_tensor("q", q, strides, sz)) || (rc = check_tensor("k", k, strides, sz)) ||
       (rc = check_tensor("v", v, strides, sz)) || (rc = check_tensor("do", dout, strides, sz)) ||
       (rc = check_tensor("dk", dk, strides, sz)) || (rc = check_tensor("dv", dv, strides, sz)))
@@ -263,7 +264,7 @@ int tattn_bwd_dq(const void* q, const void* k, const void* v, const void* dout, 
   BwdParams p{};
   int rc;
   if ((rc = bwd_common(p, strides, Z, H, N, D, dtype, sm_scale))) return rc;
-  const int sz = dtype == TATTN_F16 ? 2 : 4;
+  const int sz = dtype == TATTN_F32 ? 4 : 2;
   if ((rc = check_tensor("q", q, strides, sz)) || (rc = check_tensor("k", k, strides, sz)) ||
       (rc = check_tensor("v", v, strides, sz)) || (rc = check_tensor("do", dout, strides, sz)) ||
       (rc = check_tensor("dq", dq, strides, sz)))

@@ -50,7 +50,8 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const BwdParams p) 
     const int64_t off = hd.off + (int64_t)row * p.s[2] + ch * EPC;
     const u32x4 a = ld16((const T*)p.o + off), b = ld16((const T*)p.dout + off);
     if constexpr (EPC == 8) {
-      const f16x8 x = __builtin_bit_cast(f16x8, a), y = __builtin_bit_cast(f16x8, b);
+      using V8 = typename H16<T>::V8;
+      const V8 x = __builtin_bit_cast(V8, a), y = __builtin_bit_cast(V8, b);
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc += (float)x[i] * (float)y[i];
     } else {
@@ -105,23 +106,24 @@ struct Stage2 {
   }
 };
 
-// Natural MFMA operand (fp16): 8 halves of LDS row `row` starting at half `col` (multiple of 8).
-template <int D>
-__device__ __forceinline__ f16x8 nat_operand(const char* tile, int row, int col) {
-  return *reinterpret_cast<const TATTN_LDS f16x8*>((const TATTN_LDS char*)tile + Swz<D>::addr(row, col * 2));
+// Natural MFMA operand (16-bit types): 8 elements of LDS row `row` starting at element `col`
+// (multiple of 8).
+template <typename T, int D>
+__device__ __forceinline__ typename H16<T>::V8 nat_operand(const char* tile, int row, int col) {
+  return *reinterpret_cast<const TATTN_LDS typename H16<T>::V8*>((const TATTN_LDS char*)tile + Swz<D>::addr(row, col * 2));
 }
 
-// Transposed MFMA operand (fp16) from a perm32-ordered tile: k runs over the 16 rows of slice
-// `sl` (row 16*sl + 8*h + i for lane-half h), m/n over columns 32*u + lane%32.
-template <int D>
-__device__ __forceinline__ f16x8 tr_operand(const char* tile, int sl, int u, int lane) {
+// Transposed MFMA operand (16-bit types) from a perm32-ordered tile: k runs over the 16 rows of
+// slice `sl` (row 16*sl + 8*h + i for lane-half h), m/n over columns 32*u + lane%32.
+template <typename T, int D>
+__device__ __forceinline__ typename H16<T>::V8 tr_operand(const char* tile, int sl, int u, int lane) {
   const int g = lane >> 4, src = lane & 15;
   const int colb = (32 * u + 16 * (g & 1) + 4 * (src & 3)) * 2;
   const int row = 16 * sl + 4 * (g >> 1) + (src >> 2);  // perm32 maps row 16sl+8h+4j+t to 16sl+8j+4h+t
   const TATTN_LDS char* base = (const TATTN_LDS char*)tile;
-  const f16x4 lo = lds_read_tr(base + Swz<D>::addr(row, colb));
-  const f16x4 hi = lds_read_tr(base + Swz<D>::addr(row + 8, colb));
-  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  const auto lo = lds_tr<T>(base + Swz<D>::addr(row, colb));
+  const auto hi = lds_tr<T>(base + Swz<D>::addr(row + 8, colb));
+  return typename H16<T>::V8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
 // fp32 operand for the same role: one element per lane, row = key/query of C register r of
@@ -235,8 +237,8 @@ __global__ __launch_bounds__(NW * 64, 2) void dkdv_kernel(const BwdParams p) {
       for (int sd = 0; sd < C::NSD; ++sd) {
         Op qa, da;
         if constexpr (C::KPL == 8) {
-          qa = nat_operand<D>(qs, 32 * j + l32, sd * C::SK + C::KPL * h2);
-          da = nat_operand<D>(dos, 32 * j + l32, sd * C::SK + C::KPL * h2);
+          qa = nat_operand<T, D>(qs, 32 * j + l32, sd * C::SK + C::KPL * h2);
+          da = nat_operand<T, D>(dos, 32 * j + l32, sd * C::SK + C::KPL * h2);
         } else {
           const int off = (32 * j + l32) * St::R + (sd * C::SK + C::KPL * h2) * C::SZ;
           qa = *reinterpret_cast<const TATTN_LDS Op*>((const TATTN_LDS char*)qs + off);
@@ -282,11 +284,11 @@ __global__ __launch_bounds__(NW * 64, 2) void dkdv_kernel(const BwdParams p) {
       for (int t = 0; t < KTW; ++t) {
         if constexpr (C::KPL == 8) {
           const int j = sl >> 1, b = (sl & 1) * 8;
-          f16x8 x, y;
+          Op x, y;
 #pragma unroll
           for (int i = 0; i < 8; i += 2) {
-            const f16x2 u = pack_f16(s[t][j][b + i], s[t][j][b + i + 1]);
-            const f16x2 v = pack_f16(dp[t][j][b + i], dp[t][j][b + i + 1]);
+            const auto u = H16<T>::pack(s[t][j][b + i], s[t][j][b + i + 1]);
+            const auto v = H16<T>::pack(dp[t][j][b + i], dp[t][j][b + i + 1]);
             x[i] = u[0]; x[i + 1] = u[1];
             y[i] = v[0]; y[i + 1] = v[1];
           }
@@ -301,8 +303,8 @@ __global__ __launch_bounds__(NW * 64, 2) void dkdv_kernel(const BwdParams p) {
       for (int u = 0; u < C::DT; ++u) {
         Op dob, qb;
         if constexpr (C::KPL == 8) {
-          dob = tr_operand<D>(dos, sl, u, lane);
-          qb = tr_operand<D>(qs, sl, u, lane);
+          dob = tr_operand<T, D>(dos, sl, u, lane);
+          qb = tr_operand<T, D>(qs, sl, u, lane);
           if (D < 32 && 32 * u + 16 * ((lane >> 4) & 1) >= D) dob = qb = E::zero();
         } else {
           dob = f32_operand(dos, St::R, sl, u, lane, D);
@@ -439,8 +441,8 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_kernel(const BwdParams p) {
       for (int sd = 0; sd < C::NSD; ++sd) {
         Op ka, va;
         if constexpr (C::KPL == 8) {
-          ka = nat_operand<D>(ks, 32 * t + l32, sd * C::SK + C::KPL * h2);
-          va = nat_operand<D>(vs, 32 * t + l32, sd * C::SK + C::KPL * h2);
+          ka = nat_operand<T, D>(ks, 32 * t + l32, sd * C::SK + C::KPL * h2);
+          va = nat_operand<T, D>(vs, 32 * t + l32, sd * C::SK + C::KPL * h2);
         } else {
           const int off = (32 * t + l32) * St::R + (sd * C::SK + C::KPL * h2) * C::SZ;
           ka = *reinterpret_cast<const TATTN_LDS Op*>((const TATTN_LDS char*)ks + off);
@@ -478,10 +480,10 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_kernel(const BwdParams p) {
       for (int j = 0; j < QTW; ++j) {
         if constexpr (C::KPL == 8) {
           const int t = sl >> 1, o = (sl & 1) * 8;
-          f16x8 x;
+          Op x;
 #pragma unroll
           for (int i = 0; i < 8; i += 2) {
-            const f16x2 u = pack_f16(s[t][j][o + i], s[t][j][o + i + 1]);
+            const auto u = H16<T>::pack(s[t][j][o + i], s[t][j][o + i + 1]);
             x[i] = u[0];
             x[i + 1] = u[1];
           }
@@ -494,7 +496,7 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_kernel(const BwdParams p) {
       for (int u = 0; u < C::DT; ++u) {
         Op a;
         if constexpr (C::KPL == 8) {
-          a = tr_operand<D>(ks, sl, u, lane);
+          a = tr_operand<T, D>(ks, sl, u, lane);
           if (D < 32 && 32 * u + 16 * ((lane >> 4) & 1) >= D) a = E::zero();
         } else {
           a = f32_operand(ks, St::R, sl, u, lane, D);
@@ -545,10 +547,10 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_kernel(const BwdParams p) {
           const int d0 = 32 * u + 8 * g + 4 * h2;
           if (d0 < D) {
             if constexpr (C::KPL == 8) {
-              f16x4 x;
+              typename H16<T>::V4 x;
 #pragma unroll
-              for (int i = 0; i < 4; ++i) x[i] = (f16)(dq[u][j][4 * g + i] * p.scale);
-              *reinterpret_cast<f16x4*>(row + d0) = x;
+              for (int i = 0; i < 4; ++i) x[i] = (T)(dq[u][j][4 * g + i] * p.scale);
+              *reinterpret_cast<typename H16<T>::V4*>(row + d0) = x;
             } else {
               f32x4 x;
 #pragma unroll
@@ -581,6 +583,13 @@ int launch_bwd_preprocess(const BwdParams& p, int D, int dtype, hipStream_t st) 
       case 64: return run_preprocess<f16, 64>(p, st);
       case 128: return run_preprocess<f16, 128>(p, st);
     }
+  } else if (dtype == 2) {
+    switch (D) {
+      case 16: return run_preprocess<bf16, 16>(p, st);
+      case 32: return run_preprocess<bf16, 32>(p, st);
+      case 64: return run_preprocess<bf16, 64>(p, st);
+      case 128: return run_preprocess<bf16, 128>(p, st);
+    }
   } else {
     switch (D) {
       case 16: return run_preprocess<float, 16>(p, st);
@@ -612,12 +621,12 @@ static int launch_dkdv_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(e.nw * 64);
   if constexpr (e.pipe == 1) {
-    static_assert(std::is_same<T, f16>::value && D <= 64 && e.tiles == 1 && e.other == 32, "pipelined dK/dV shape");
+    static_assert(sizeof(T) == 2 && D <= 64 && e.tiles == 1 && e.other == 32, "pipelined dK/dV shape");
     if (slice_fits32(p, D)) {
       if (causal)
-        dkdv_pipe_kernel<D, e.nw, e.occ, true><<<grid, block, 0, st>>>(p);
+        dkdv_pipe_kernel<T, D, e.nw, e.occ, true><<<grid, block, 0, st>>>(p);
       else
-        dkdv_pipe_kernel<D, e.nw, e.occ, false><<<grid, block, 0, st>>>(p);
+        dkdv_pipe_kernel<T, D, e.nw, e.occ, false><<<grid, block, 0, st>>>(p);
       return check_launch("tattn_bwd_dkdv");
     }
     p.n_blocks = (p.N + 127) / 128;  // slices beyond 2 GiB: 64-bit addressing
@@ -645,12 +654,12 @@ static int launch_dq_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(e.nw * 64);
   if constexpr (e.pipe == 1) {
-    static_assert(std::is_same<T, f16>::value && D <= 64 && e.tiles == 1 && e.other == 32, "pipelined dQ shape");
+    static_assert(sizeof(T) == 2 && D <= 64 && e.tiles == 1 && e.other == 32, "pipelined dQ shape");
     if (slice_fits32(p, D)) {
       if (causal)
-        dq_pipe_kernel<D, e.nw, e.occ, true><<<grid, block, 0, st>>>(p);
+        dq_pipe_kernel<T, D, e.nw, e.occ, true><<<grid, block, 0, st>>>(p);
       else
-        dq_pipe_kernel<D, e.nw, e.occ, false><<<grid, block, 0, st>>>(p);
+        dq_pipe_kernel<T, D, e.nw, e.occ, false><<<grid, block, 0, st>>>(p);
       return check_launch("tattn_bwd_dq");
     }
     p.n_blocks = (p.N + 127) / 128;  // slices beyond 2 GiB: 64-bit addressing
@@ -692,6 +701,13 @@ static int dispatch_dq(int id, const BwdParams& p, bool causal, hipStream_t st, 
       case 64: return FN<f16, 64>(id, p, causal, st, std::make_index_sequence<TABLE<f16, 64>::n>{}); \
       case 128: return FN<f16, 128>(id, p, causal, st, std::make_index_sequence<TABLE<f16, 128>::n>{}); \
     }                                                                                            \
+  } else if (dtype == 2) {                                                                       \
+    switch (D) {                                                                                 \
+      case 16: return FN<bf16, 16>(id, p, causal, st, std::make_index_sequence<TABLE<bf16, 16>::n>{}); \
+      case 32: return FN<bf16, 32>(id, p, causal, st, std::make_index_sequence<TABLE<bf16, 32>::n>{}); \
+      case 64: return FN<bf16, 64>(id, p, causal, st, std::make_index_sequence<TABLE<bf16, 64>::n>{}); \
+      case 128: return FN<bf16, 128>(id, p, causal, st, std::make_index_sequence<TABLE<bf16, 128>::n>{}); \
+    }                                                                                            \
   } else {                                                                                       \
     switch (D) {                                                                                 \
       case 16: return FN<float, 16>(id, p, causal, st, std::make_index_sequence<TABLE<float, 16>::n>{}); \
@@ -711,13 +727,13 @@ int launch_bwd_dq(const BwdParams& p, int D, int dtype, bool causal, int id, hip
 }
 
 int dkdv_lds_bytes(int D, int dtype, const TileEntry& e) {
-  const int r = dtype == 0 ? (D < 32 ? 64 : 2 * D) : 4 * D + 16;
+  const int r = dtype != 1 ? (D < 32 ? 64 : 2 * D) : 4 * D + 16;
   if (e.pipe) return 4 * (2 * 32 * r + 256);
   return 2 * (2 * e.other * r + 2 * e.other * 4);
 }
 
 int dq_lds_bytes(int D, int dtype, const TileEntry& e) {
-  const int r = dtype == 0 ? (D < 32 ? 64 : 2 * D) : 4 * D + 16;
+  const int r = dtype != 1 ? (D < 32 ? 64 : 2 * D) : 4 * D + 16;
   if (e.pipe) return 4 * (2 * 32 * r);
   return 2 * (2 * e.other * r);
 }

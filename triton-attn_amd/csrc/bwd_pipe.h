@@ -1,4 +1,4 @@
-// Software-pipelined fp16 backward kernels for gfx950 (head dims 16, 32, 64).
+// Software-pipelined 16-bit (fp16, bf16) backward kernels for gfx950 (head dims 16, 32, 64).
 //
 // Same math and rounding points as the generic kernels in bwd.hip (the reference's
 // src/tattn/kernels.py:151-321); the difference is the schedule. Each 32-row step issues
@@ -48,21 +48,27 @@ __device__ __forceinline__ void tr_addrs(int sl, int u, int lane, int& a0, int& 
   a1 = Swz<D>::addr(row + 8, colb);
 }
 
-__device__ __forceinline__ f16x8 tr_pair(const char* base, int a0, int a1) {
-  const f16x4 lo = lds_read_tr((const TATTN_LDS char*)base + a0);
-  const f16x4 hi = lds_read_tr((const TATTN_LDS char*)base + a1);
-  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+template <typename T>
+__device__ __forceinline__ typename H16<T>::V8 tr_pair(const char* base, int a0, int a1) {
+  const auto lo = lds_tr<T>((const TATTN_LDS char*)base + a0);
+  const auto hi = lds_tr<T>((const TATTN_LDS char*)base + a1);
+  return typename H16<T>::V8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-__device__ __forceinline__ f16x8 lds8(const char* p) {
-  return *reinterpret_cast<const TATTN_LDS f16x8*>((const TATTN_LDS char*)p);
+template <typename T>
+__device__ __forceinline__ typename H16<T>::V8 lds8(const char* p) {
+  return *reinterpret_cast<const TATTN_LDS typename H16<T>::V8*>((const TATTN_LDS char*)p);
 }
 
 template <int N> using IC = std::integral_constant<int, N>;
 
 // ---- dK / dV --------------------------------------------------------------------------------
-template <int D, int NW, int OCC, bool CAUSAL>
+template <typename T, int D, int NW, int OCC, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams p) {
+  using H = H16<T>;
+  using V8 = typename H::V8;
+  using V4 = typename H::V4;
+  using V2 = typename H::V2;
   using B = BwdPipe<D>;
   constexpr int NT = NW * 64, BNK = NW * 32;
   constexpr int STAGE = B::DKDV_STAGE;
@@ -84,16 +90,16 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
   const int lo = CAUSAL ? kblk : 0;
   const int nsteps = (N - lo + 31) / 32;
 
-  f16x8 kop[NSD], vop[NSD];
+  V8 kop[NSD], vop[NSD];
   {
     const int key = kw0 + l32;
     const int64_t off = hoff + (int64_t)(key < N ? key : 0) * rs + 8 * h2;
 #pragma unroll
     for (int s = 0; s < NSD; ++s) {
-      const f16x8 a = *reinterpret_cast<const f16x8*>((const f16*)p.k + off + 16 * s);
-      const f16x8 b = *reinterpret_cast<const f16x8*>((const f16*)p.v + off + 16 * s);
-      kop[s] = key < N ? a : f16x8{};
-      vop[s] = key < N ? b : f16x8{};
+      const V8 a = *reinterpret_cast<const V8*>((const T*)p.k + off + 16 * s);
+      const V8 b = *reinterpret_cast<const V8*>((const T*)p.v + off + 16 * s);
+      kop[s] = key < N ? a : V8{};
+      vop[s] = key < N ? b : V8{};
     }
   }
   f32x16 dk[DT], dv[DT];
@@ -101,8 +107,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
   for (int u = 0; u < DT; ++u) dk[u] = dv[u] = f32x16{};
 
   // HBM: Q, dO rows and M, delta entries from query `lo` on.
-  const __amdgpu_buffer_rsrc_t qrs = slice_rsrc((const f16*)p.q + hoff + (int64_t)lo * rs, slice_bytes(N - lo, rs, D));
-  const __amdgpu_buffer_rsrc_t ors = slice_rsrc((const f16*)p.dout + hoff + (int64_t)lo * rs, slice_bytes(N - lo, rs, D));
+  const __amdgpu_buffer_rsrc_t qrs = slice_rsrc((const T*)p.q + hoff + (int64_t)lo * rs, slice_bytes(N - lo, rs, D));
+  const __amdgpu_buffer_rsrc_t ors = slice_rsrc((const T*)p.dout + hoff + (int64_t)lo * rs, slice_bytes(N - lo, rs, D));
   const __amdgpu_buffer_rsrc_t mrs = slice_rsrc(p.m + (int64_t)zh * N + lo, (uint64_t)(N - lo) * 4);
   const __amdgpu_buffer_rsrc_t drs = slice_rsrc(p.delta + (int64_t)zh * N + lo, (uint64_t)(N - lo) * 4);
   const uint32_t step_bytes = uniform32((uint32_t)(rs * 64));
@@ -162,26 +168,26 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
     dp = f32x16{};
 #pragma unroll
     for (int sd = 0; sd < NSD; ++sd) {
-      s = Elt<f16>::mfma(lds8(base + nat[sd]), kop[sd], s);
-      dp = Elt<f16>::mfma(lds8(base + B::TILE + nat[sd]), vop[sd], dp);
+      s = Elt<T>::mfma(lds8<T>(base + nat[sd]), kop[sd], s);
+      dp = Elt<T>::mfma(lds8<T>(base + B::TILE + nat[sd]), vop[sd], dp);
     }
   };
   // dV += P^T dO, dK += dS^T Q over the stage's 32 queries.
-  auto grad_mma = [&](const f16x8* pp, const f16x8* dsp, int st) {
+  auto grad_mma = [&](const V8* pp, const V8* dsp, int st) {
     const char* base = smem + st * STAGE;
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl)
 #pragma unroll
       for (int u = 0; u < DT; ++u) {
-        f16x8 dob = tr_pair(base + B::TILE, tra[sl][u][0], tra[sl][u][1]);
-        f16x8 qb = tr_pair(base, tra[sl][u][0], tra[sl][u][1]);
-        if (D < 32 && 16 * ((lane >> 4) & 1) >= D) dob = qb = f16x8{};
-        dv[u] = Elt<f16>::mfma(pp[sl], dob, dv[u]);
-        dk[u] = Elt<f16>::mfma(dsp[sl], qb, dk[u]);
+        V8 dob = tr_pair<T>(base + B::TILE, tra[sl][u][0], tra[sl][u][1]);
+        V8 qb = tr_pair<T>(base, tra[sl][u][0], tra[sl][u][1]);
+        if (D < 32 && 16 * ((lane >> 4) & 1) >= D) dob = qb = V8{};
+        dv[u] = Elt<T>::mfma(pp[sl], dob, dv[u]);
+        dk[u] = Elt<T>::mfma(dsp[sl], qb, dk[u]);
       }
   };
   // P = exp2(S c - M), dS = P (dP - delta) for the stage's queries, rounded into MFMA operands.
-  auto pds = [&](const f32x16& s, const f32x16& dp, f16x8* pp, f16x8* dsp, int st, int q0, auto mask_tag) {
+  auto pds = [&](const f32x16& s, const f32x16& dp, V8* pp, V8* dsp, int st, int q0, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const char* base = smem + st * STAGE;
     const int key = kw0 + l32;
@@ -191,7 +197,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
       const f32x4 m1 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 64 * a + 16);
       const f32x4 d0 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 128 + 64 * a);
       const f32x4 d1 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 128 + 64 * a + 16);
-      f16x8 x, y;
+      V8 x, y;
 #pragma unroll
       for (int i = 0; i < 8; i += 2) {
         float pr[2], dr[2];
@@ -205,7 +211,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
           pr[e] = pv;
           dr[e] = pv * (dp[r] - dl);
         }
-        const f16x2 ph = pack_f16(pr[0], pr[1]), dh = pack_f16(dr[0], dr[1]);
+        const V2 ph = H::pack(pr[0], pr[1]), dh = H::pack(dr[0], dr[1]);
         x[i] = ph[0];
         x[i + 1] = ph[1];
         y[i] = dh[0];
@@ -231,12 +237,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
   __syncthreads();
 
   f32x16 sa, da, sb, db;
-  f16x8 pa[2] = {}, dsa[2] = {}, pb[2], dsb[2];
+  V8 pa[2] = {}, dsa[2] = {}, pb[2], dsb[2];
   qk(sa, da, 0);
 
   // One step: S/dP of step i+1, dV/dK of step i-1, P/dS of step i; ST = i % 4 (or -1: run time).
   auto step = [&](int i, int st, f32x16& scur, f32x16& dcur, f32x16& snext, f32x16& dnext,
-                  const f16x8* pprev, const f16x8* dsprev, f16x8* pcur, f16x8* dscur, auto mask_tag) {
+                  const V8* pprev, const V8* dsprev, V8* pcur, V8* dscur, auto mask_tag) {
     gload(i + 2);
     qk(snext, dnext, (st + 1) & 3);
     grad_mma(pprev, dsprev, (st + 3) & 3);
@@ -273,8 +279,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
   grad_mma(pa, dsa, (nsteps - 1) & 3);
 
   // Store: C register r of lane holds key 8*(r/4) + 4*h2 + r%4 of the wave, column 32u + l32.
-  f16* DK = (f16*)p.dk + hoff;
-  f16* DV = (f16*)p.dv + hoff;
+  T* DK = (T*)p.dk + hoff;
+  T* DV = (T*)p.dv + hoff;
 #pragma unroll
   for (int u = 0; u < DT; ++u) {
     const int d = 32 * u + l32;
@@ -283,8 +289,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
       for (int r = 0; r < 16; ++r) {
         const int key = kw0 + 8 * (r >> 2) + 4 * h2 + (r & 3);
         if (key < N) {
-          DK[(int64_t)key * rs + d] = (f16)(dk[u][r] * p.scale);
-          DV[(int64_t)key * rs + d] = (f16)dv[u][r];
+          DK[(int64_t)key * rs + d] = (T)(dk[u][r] * p.scale);
+          DV[(int64_t)key * rs + d] = (T)dv[u][r];
         }
       }
     }
@@ -292,8 +298,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
 }
 
 // ---- dQ ----------------------------------------------------------------------------------
-template <int D, int NW, int OCC, bool CAUSAL>
+template <typename T, int D, int NW, int OCC, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p) {
+  using H = H16<T>;
+  using V8 = typename H::V8;
+  using V4 = typename H::V4;
+  using V2 = typename H::V2;
   using B = BwdPipe<D>;
   constexpr int NT = NW * 64, BMQ = NW * 32;
   constexpr int STAGE = B::DQ_STAGE;
@@ -315,15 +325,15 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
   const int qw0 = qblk + 32 * w;
   const int q = qw0 + l32;
 
-  f16x8 qop[NSD], dop[NSD];
+  V8 qop[NSD], dop[NSD];
   {
     const int64_t off = hoff + (int64_t)(q < N ? q : 0) * rs + 8 * h2;
 #pragma unroll
     for (int s = 0; s < NSD; ++s) {
-      const f16x8 a = *reinterpret_cast<const f16x8*>((const f16*)p.q + off + 16 * s);
-      const f16x8 b = *reinterpret_cast<const f16x8*>((const f16*)p.dout + off + 16 * s);
-      qop[s] = q < N ? a : f16x8{};
-      dop[s] = q < N ? b : f16x8{};
+      const V8 a = *reinterpret_cast<const V8*>((const T*)p.q + off + 16 * s);
+      const V8 b = *reinterpret_cast<const V8*>((const T*)p.dout + off + 16 * s);
+      qop[s] = q < N ? a : V8{};
+      dop[s] = q < N ? b : V8{};
     }
   }
   const float nm = -(q < N ? p.m[(int64_t)zh * N + q] : 0.0f);
@@ -339,8 +349,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
   // Steps before n_full need no mask for any wave of the workgroup.
   const int n_full = CAUSAL ? min((qblk + 1) / 32, N / 32) : N / 32;
 
-  const __amdgpu_buffer_rsrc_t krs = slice_rsrc((const f16*)p.k + hoff, slice_bytes(N, rs, D));
-  const __amdgpu_buffer_rsrc_t vrs = slice_rsrc((const f16*)p.v + hoff, slice_bytes(N, rs, D));
+  const __amdgpu_buffer_rsrc_t krs = slice_rsrc((const T*)p.k + hoff, slice_bytes(N, rs, D));
+  const __amdgpu_buffer_rsrc_t vrs = slice_rsrc((const T*)p.v + hoff, slice_bytes(N, rs, D));
   const uint32_t step_bytes = uniform32((uint32_t)(rs * 64));
   uint32_t goff[CPT];
   int ldst[CPT];
@@ -386,27 +396,27 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
     dp = f32x16{};
 #pragma unroll
     for (int sd = 0; sd < NSD; ++sd) {
-      s = Elt<f16>::mfma(lds8(base + nat[sd]), qop[sd], s);
-      dp = Elt<f16>::mfma(lds8(base + B::TILE + nat[sd]), dop[sd], dp);
+      s = Elt<T>::mfma(lds8<T>(base + nat[sd]), qop[sd], s);
+      dp = Elt<T>::mfma(lds8<T>(base + B::TILE + nat[sd]), dop[sd], dp);
     }
   };
   // dQ^T += K^T dS^T over the stage's 32 keys.
-  auto dq_mma = [&](const f16x8* dsp, int st) {
+  auto dq_mma = [&](const V8* dsp, int st) {
     const char* base = smem + st * STAGE;
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl)
 #pragma unroll
       for (int u = 0; u < DT; ++u) {
-        f16x8 a = tr_pair(base, tra[sl][u][0], tra[sl][u][1]);
-        if (D < 32 && 16 * ((lane >> 4) & 1) >= D) a = f16x8{};
-        dq[u] = Elt<f16>::mfma(a, dsp[sl], dq[u]);
+        V8 a = tr_pair<T>(base, tra[sl][u][0], tra[sl][u][1]);
+        if (D < 32 && 16 * ((lane >> 4) & 1) >= D) a = V8{};
+        dq[u] = Elt<T>::mfma(a, dsp[sl], dq[u]);
       }
   };
-  auto dsv = [&](const f32x16& s, const f32x16& dp, f16x8* dsp, int kb, auto mask_tag) {
+  auto dsv = [&](const f32x16& s, const f32x16& dp, V8* dsp, int kb, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
-      f16x8 x;
+      V8 x;
 #pragma unroll
       for (int i = 0; i < 8; i += 2) {
         float dr[2];
@@ -420,7 +430,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
           }
           dr[e] = pv2 * (dp[r] - dl);
         }
-        const f16x2 dh = pack_f16(dr[0], dr[1]);
+        const V2 dh = H::pack(dr[0], dr[1]);
         x[i] = dh[0];
         x[i + 1] = dh[1];
       }
@@ -438,11 +448,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
   __syncthreads();
 
   f32x16 sa, da, sb, db;
-  f16x8 ea[2] = {}, eb[2];
+  V8 ea[2] = {}, eb[2];
   if (wave_steps > 0) qk(sa, da, 0);
 
   auto full_step = [&](int i, int st, f32x16& scur, f32x16& dcur, f32x16& snext, f32x16& dnext,
-                       const f16x8* eprev, f16x8* ecur) {
+                       const V8* eprev, V8* ecur) {
     gload(i + 2);
     qk(snext, dnext, (st + 1) & 3);
     dq_mma(eprev, (st + 3) & 3);
@@ -479,17 +489,17 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
   if (wave_steps == nsteps && nsteps > 0) dq_mma(ea, (nsteps - 1) & 3);
 
   if (q < N) {
-    f16* row = (f16*)p.dq + hoff + (int64_t)q * rs;
+    T* row = (T*)p.dq + hoff + (int64_t)q * rs;
 #pragma unroll
     for (int u = 0; u < DT; ++u)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d0 = 32 * u + 8 * g + 4 * h2;
         if (d0 < D) {
-          f16x4 x;
+          V4 x;
 #pragma unroll
-          for (int i2 = 0; i2 < 4; ++i2) x[i2] = (f16)(dq[u][4 * g + i2] * p.scale);
-          *reinterpret_cast<f16x4*>(row + d0) = x;
+          for (int i2 = 0; i2 < 4; ++i2) x[i2] = (T)(dq[u][4 * g + i2] * p.scale);
+          *reinterpret_cast<V4*>(row + d0) = x;
         }
       }
   }

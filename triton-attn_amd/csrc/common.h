@@ -20,6 +20,10 @@ typedef _Float16 f16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -39,6 +43,15 @@ template <> struct Elt<f16> {
   typedef f16x8 Op;
   static __device__ __forceinline__ f32x16 mfma(Op a, Op b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ Op zero() { return Op{}; }
+};
+
+template <> struct Elt<bf16> {
+  static constexpr int KPL = 8;
+  typedef bf16x8 Op;
+  static __device__ __forceinline__ f32x16 mfma(Op a, Op b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ Op zero() { return Op{}; }
 };
@@ -78,6 +91,29 @@ __device__ __forceinline__ f16x2 pack_f16(float a, float b) {
   return f16x2{(f16)a, (f16)b};
 }
 
+// 16-bit element types (fp16, bf16): operand vectors, the round-to-nearest-even pack of two
+// floats (v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32) and the sum of a packed pair into a float
+// accumulator (v_dot2 with (1, 1): exact products, one fp32 rounding).
+template <typename T> struct H16;
+template <> struct H16<f16> {
+  typedef f16x2 V2;
+  typedef f16x4 V4;
+  typedef f16x8 V8;
+  static __device__ __forceinline__ V2 pack(float a, float b) { return V2{(f16)a, (f16)b}; }
+  static __device__ __forceinline__ float sum2(V2 x, float acc) {
+    return __builtin_amdgcn_fdot2(x, V2{(f16)1.0f, (f16)1.0f}, acc, false);
+  }
+};
+template <> struct H16<bf16> {
+  typedef bf16x2 V2;
+  typedef bf16x4 V4;
+  typedef bf16x8 V8;
+  static __device__ __forceinline__ V2 pack(float a, float b) { return V2{(bf16)a, (bf16)b}; }
+  static __device__ __forceinline__ float sum2(V2 x, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(x, V2{(bf16)1.0f, (bf16)1.0f}, acc, false);
+  }
+};
+
 // Key permutation inside a 32-row tile: swaps bits 2 and 3 of the row index. Storing key r of
 // a tile at LDS row perm32(r) makes the MFMA C layout hand every lane-half 8 consecutive keys
 // per 16-key slice: C register r of lane-half h then holds key kappa(r, h).
@@ -99,6 +135,11 @@ __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4
 __device__ __forceinline__ f16x4 lds_read_tr(const TATTN_LDS char* p) {
   i16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TATTN_LDS i16x4*)(p));
   return __builtin_bit_cast(f16x4, t);
+}
+template <typename T>
+__device__ __forceinline__ typename H16<T>::V4 lds_tr(const TATTN_LDS char* p) {
+  i16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TATTN_LDS i16x4*)(p));
+  return __builtin_bit_cast(typename H16<T>::V4, t);
 }
 
 struct FwdParams {

@@ -206,10 +206,10 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_generic_kernel(const FwdParams
 #pragma unroll
         for (int sg = 0; sg < C::NSK; ++sg) {
           const int t = sg >> 1, b = (sg & 1) * 8;
-          f16x8 x;
+          typename H16<T>::V8 x;
 #pragma unroll
           for (int i = 0; i < 8; i += 2) {
-            f16x2 pr = pack_f16(s[t][j][b + i], s[t][j][b + i + 1]);
+            const typename H16<T>::V2 pr = H16<T>::pack(s[t][j][b + i], s[t][j][b + i + 1]);
             x[i] = pr[0];
             x[i + 1] = pr[1];
           }
@@ -231,8 +231,8 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_generic_kernel(const FwdParams
           const int kb0 = 16 * sg + 8 * (g >> 1);
           const TATTN_LDS char* a =
               (const TATTN_LDS char*)vs + (kb0 + (src >> 2)) * C::RV + (mb + 4 * (src & 3)) * 2;
-          const f16x4 lo = lds_read_tr(a), hi4 = lds_read_tr(a + 4 * C::RV);
-          vop = f16x8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+          const auto lo = lds_tr<T>(a), hi4 = lds_tr<T>(a + 4 * C::RV);
+          vop = Op{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
           if (D < 32 && mb >= D) vop = E::zero();
         } else {
           const int d = 32 * u + l32;
@@ -283,10 +283,10 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_generic_kernel(const FwdParams
           const int d0 = 32 * u + 8 * g + 4 * h2;
           if (d0 < D) {
             if constexpr (C::KPL == 8) {
-              f16x4 x;
+              typename H16<T>::V4 x;
 #pragma unroll
-              for (int i = 0; i < 4; ++i) x[i] = (f16)(acc[u][j][4 * g + i] * inv);
-              *reinterpret_cast<f16x4*>(orow + d0) = x;
+              for (int i = 0; i < 4; ++i) x[i] = (T)(acc[u][j][4 * g + i] * inv);
+              *reinterpret_cast<typename H16<T>::V4*>(orow + d0) = x;
             } else {
               f32x4 x;
 #pragma unroll
@@ -334,8 +334,12 @@ struct PipeLayout {
   static constexpr int LDS = NSLOT * (KSLOT + VSLOT);
 };
 
-template <int D, int NW, int QT, int OCC, bool CAUSAL>
+template <typename T, int D, int NW, int QT, int OCC, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams p) {
+  using H = H16<T>;
+  using V8 = typename H::V8;
+  using V4 = typename H::V4;
+  using V2 = typename H::V2;
   using L = PipeLayout<D>;
   constexpr int NT = NW * 64, BM = NW * QT * 32;
   constexpr int NSD = D / 16;        // 16-wide d slices of S = K Q^T
@@ -359,27 +363,27 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   int qb = blockIdx.x / zhs;
   if (CAUSAL) qb = p.n_qblocks - 1 - qb;  // longest rows first
   const int64_t z = zh / p.H, hh = zh % p.H;
-  const f16* Q = (const f16*)p.q + z * p.sq[0] + hh * p.sq[1];
-  f16* O = (f16*)p.o + z * p.so[0] + hh * p.so[1];
+  const T* Q = (const T*)p.q + z * p.sq[0] + hh * p.sq[1];
+  T* O = (T*)p.o + z * p.so[0] + hh * p.so[1];
   float* M = p.m ? p.m + (int64_t)zh * N : nullptr;  // null: M not stored
   const int64_t sqn = p.sq[2], son = p.so[2];
-  const __amdgpu_buffer_rsrc_t krs = slice_rsrc((const f16*)p.k + z * p.sk[0] + hh * p.sk[1], slice_bytes(N, p.sk[2], D));
-  const __amdgpu_buffer_rsrc_t vrs = slice_rsrc((const f16*)p.v + z * p.sv[0] + hh * p.sv[1], slice_bytes(N, p.sv[2], D));
+  const __amdgpu_buffer_rsrc_t krs = slice_rsrc((const T*)p.k + z * p.sk[0] + hh * p.sk[1], slice_bytes(N, p.sk[2], D));
+  const __amdgpu_buffer_rsrc_t vrs = slice_rsrc((const T*)p.v + z * p.sv[0] + hh * p.sv[1], slice_bytes(N, p.sv[2], D));
   const uint32_t k_step = uniform32((uint32_t)(p.sk[2] * 64)), v_step = uniform32((uint32_t)(p.sv[2] * 64));
   const float c = p.c;
 
   const int qblk = qb * BM;
   const int qw0 = qblk + w * QT * 32;
 
-  f16x8 qop[QT][NSD];
+  V8 qop[QT][NSD];
 #pragma unroll
   for (int j = 0; j < QT; ++j) {
     const int row = qw0 + 32 * j + l32;
-    const f16* src = Q + (int64_t)(row < N ? row : 0) * sqn + 8 * h2;
+    const T* src = Q + (int64_t)(row < N ? row : 0) * sqn + 8 * h2;
 #pragma unroll
     for (int s = 0; s < NSD; ++s) {
-      const f16x8 x = *reinterpret_cast<const f16x8*>(src + 16 * s);
-      qop[j][s] = row < N ? x : f16x8{};
+      const V8 x = *reinterpret_cast<const V8*>(src + 16 * s);
+      qop[j][s] = row < N ? x : V8{};
     }
   }
 
@@ -445,9 +449,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
     for (int j = 0; j < QT; ++j) s[j] = f32x16{};
 #pragma unroll
     for (int sd = 0; sd < NSD; ++sd) {
-      const f16x8 kop = *reinterpret_cast<const TATTN_LDS f16x8*>((const TATTN_LDS char*)kbuf(kb_) + kop_off + 32 * sd);
+      const V8 kop = *reinterpret_cast<const TATTN_LDS V8*>((const TATTN_LDS char*)kbuf(kb_) + kop_off + 32 * sd);
 #pragma unroll
-      for (int j = 0; j < QT; ++j) s[j] = Elt<f16>::mfma(kop, qop[j][sd], s[j]);
+      for (int j = 0; j < QT; ++j) s[j] = Elt<T>::mfma(kop, qop[j][sd], s[j]);
     }
   };
 
@@ -460,27 +464,26 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
 #pragma unroll
     for (int u = 0; u < DT; ++u) acc[u][j] = f32x16{};
   }
-  const f16x2 ones = {(f16)1.0f, (f16)1.0f};
 
   // O^T += V^T P^T for the 32-key tile in V buffer vb_.
-  auto pv_mma = [&](const f16x8 (*pp)[2], int vb_) {
+  auto pv_mma = [&](const V8 (*pp)[2], int vb_) {
 #pragma unroll
     for (int u = 0; u < DT; ++u) {
 #pragma unroll
       for (int sg = 0; sg < 2; ++sg) {
         const TATTN_LDS char* a = (const TATTN_LDS char*)vbuf(vb_) + vop_off + 16 * sg * L::RV + 64 * u;
-        const f16x4 lo = lds_read_tr(a), hi4 = lds_read_tr(a + 4 * L::RV);
-        f16x8 vop = f16x8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-        if (D < 32 && 32 * u + 16 * (g & 1) >= D) vop = f16x8{};
+        const V4 lo = lds_tr<T>(a), hi4 = lds_tr<T>(a + 4 * L::RV);
+        V8 vop = V8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+        if (D < 32 && 32 * u + 16 * (g & 1) >= D) vop = V8{};
 #pragma unroll
-        for (int j = 0; j < QT; ++j) acc[u][j] = Elt<f16>::mfma(vop, pp[j][sg], acc[u][j]);
+        for (int j = 0; j < QT; ++j) acc[u][j] = Elt<T>::mfma(vop, pp[j][sg], acc[u][j]);
       }
     }
   };
 
   // Softmax of scur (keys kb..kb+31): probabilities into pc, running max and sum updated;
   // returns whether any row of the wave raised its max (the accumulator then needs alpha).
-  auto softmax = [&](f32x16* scur, f16x8 (*pc)[2], float* alpha, int kb, auto mask_tag) {
+  auto softmax = [&](f32x16* scur, V8 (*pc)[2], float* alpha, int kb, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     if constexpr (MASK) {
 #pragma unroll
@@ -510,13 +513,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
       float ps = 0.0f;
 #pragma unroll
       for (int sg = 0; sg < 2; ++sg) {
-        f16x8 x;
+        V8 x;
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
           const float e0 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i], c, nm));
           const float e1 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i + 1], c, nm));
-          const f16x2 pr = pack_f16(e0, e1);
-          ps = __builtin_amdgcn_fdot2(pr, ones, ps, false);
+          const V2 pr = H::pack(e0, e1);
+          ps = H::sum2(pr, ps);
           x[i] = pr[0];
           x[i + 1] = pr[1];
         }
@@ -540,7 +543,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   // wave down the slow path (fast_fixup): row max, lazy update, accumulator rescale,
   // probabilities recomputed. Probabilities fed to the MFMAs therefore stay at or below 2^12,
   // far inside fp16, and rows whose max moves by less than that skip the max entirely.
-  auto fast_probs = [&](f32x16* scur, f16x8 (*pc)[2], float* ps) {
+  auto fast_probs = [&](f32x16* scur, V8 (*pc)[2], float* ps) {
     bool need = false;
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
@@ -548,13 +551,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
       float acc_s = 0.0f;
 #pragma unroll
       for (int sg = 0; sg < 2; ++sg) {
-        f16x8 x;
+        V8 x;
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
           const float e0 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i], c, nm));
           const float e1 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i + 1], c, nm));
-          const f16x2 pr = pack_f16(e0, e1);
-          acc_s = __builtin_amdgcn_fdot2(pr, ones, acc_s, false);
+          const V2 pr = H::pack(e0, e1);
+          acc_s = H::sum2(pr, acc_s);
           x[i] = pr[0];
           x[i + 1] = pr[1];
         }
@@ -569,7 +572,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   // need not stay live through the fast path. The slow path is the body of a one-sided branch
   // (the fast path's state updates come first and are undone there): a two-sided branch that
   // updates the accumulators on one side only makes the register allocator double them.
-  auto fast_fixup = [&](bool need, f32x16* scur, f16x8 (*pc)[2], const float* ps, int kc_) {
+  auto fast_fixup = [&](bool need, f32x16* scur, V8 (*pc)[2], const float* ps, int kc_) {
     float lprev[QT];
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
@@ -598,9 +601,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   __syncthreads();
 
   f32x16 sa[QT], sb[QT];
-  f16x8 pa[QT][2], pb[QT][2];
+  V8 pa[QT][2], pb[QT][2];
 #pragma unroll
-  for (int j = 0; j < QT; ++j) pa[j][0] = pa[j][1] = f16x8{};
+  for (int j = 0; j < QT; ++j) pa[j][0] = pa[j][1] = V8{};
   if (wave_steps > 0) qk(sa, 0);
 
   // Steps before n_full need no mask for any wave of the workgroup (all keys below the
@@ -614,7 +617,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   // K_{i+3} and V_{i+1} start streaming into the slots freed two steps ago. The instruction
   // order within the step is left to the compiler (measured faster than pinned MFMA/VALU
   // interleave patterns).
-  auto full_step = [&](int i, f32x16* scur, f32x16* snext, const f16x8 (*pprev)[2], f16x8 (*pcur)[2],
+  auto full_step = [&](int i, f32x16* scur, f32x16* snext, const V8 (*pprev)[2], V8 (*pcur)[2],
                        auto iv_tag) {
     constexpr int IV = decltype(iv_tag)::value;
     dma(i + 3, i + 1, (IV + 3) % 4, (IV + 1) % 4);
@@ -667,17 +670,17 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
     const float inv = 1.0f / lt;
     const int q = qw0 + 32 * j + l32;
     if (q < N) {
-      f16* orow = O + (int64_t)q * son;
+      T* orow = O + (int64_t)q * son;
 #pragma unroll
       for (int u = 0; u < DT; ++u)
 #pragma unroll
         for (int g2 = 0; g2 < 4; ++g2) {
           const int d0 = 32 * u + 8 * g2 + 4 * h2;
           if (d0 < D) {
-            f16x4 x;
+            V4 x;
 #pragma unroll
-            for (int i2 = 0; i2 < 4; ++i2) x[i2] = (f16)(acc[u][j][4 * g2 + i2] * inv);
-            *reinterpret_cast<f16x4*>(orow + d0) = x;
+            for (int i2 = 0; i2 < 4; ++i2) x[i2] = (T)(acc[u][j][4 * g2 + i2] * inv);
+            *reinterpret_cast<V4*>(orow + d0) = x;
           }
         }
       if (h2 == 0 && M) M[q] = mrow[j] + __log2f(lt);
@@ -698,8 +701,8 @@ static int launch_fwd_entry(const FwdParams& p0, bool causal, hipStream_t st) {
   const dim3 grid((unsigned)blocks), block(e.nw * 64);
   const bool fits32 = slice_bytes(p.N, p.sk[2], D) + (uint64_t)p.sk[2] * 128 < (1ull << 31) &&
                       slice_bytes(p.N, p.sv[2], D) + (uint64_t)p.sv[2] * 128 < (1ull << 31);
-  if constexpr (std::is_same<T, f16>::value) {
-    static_assert(e.other == 32, "the fp16 forward runs 32 keys per step");
+  if constexpr (sizeof(T) == 2) {  // fp16, bf16: the pipelined kernel
+    static_assert(e.other == 32, "the 16-bit forward runs 32 keys per step");
     if (!fits32) {  // slices beyond 2 GiB: 64-bit addressing
       if (causal)
         fwd_generic_kernel<T, D, 4, 1, 64, true><<<dim3((unsigned)(((p.N + 127) / 128) * (int64_t)p.Z * p.H)), dim3(256), 0, st>>>(
@@ -710,9 +713,9 @@ static int launch_fwd_entry(const FwdParams& p0, bool causal, hipStream_t st) {
       return check_launch("tattn_fwd");
     }
     if (causal)
-      fwd_pipe_kernel<D, e.nw, e.tiles, e.occ, true><<<grid, block, 0, st>>>(p);
+      fwd_pipe_kernel<T, D, e.nw, e.tiles, e.occ, true><<<grid, block, 0, st>>>(p);
     else
-      fwd_pipe_kernel<D, e.nw, e.tiles, e.occ, false><<<grid, block, 0, st>>>(p);
+      fwd_pipe_kernel<T, D, e.nw, e.tiles, e.occ, false><<<grid, block, 0, st>>>(p);
   } else {
     if (causal)
       fwd_generic_kernel<T, D, e.nw, e.tiles, e.other, true><<<grid, block, 0, st>>>(p);
@@ -743,6 +746,13 @@ int launch_fwd(const FwdParams& p, int D, int dtype, bool causal, int id, hipStr
       case 64: return run_fwd_d<f16, 64>(id, p, causal, st);
       case 128: return run_fwd_d<f16, 128>(id, p, causal, st);
     }
+  } else if (dtype == 2) {
+    switch (D) {
+      case 16: return run_fwd_d<bf16, 16>(id, p, causal, st);
+      case 32: return run_fwd_d<bf16, 32>(id, p, causal, st);
+      case 64: return run_fwd_d<bf16, 64>(id, p, causal, st);
+      case 128: return run_fwd_d<bf16, 128>(id, p, causal, st);
+    }
   } else {
     switch (D) {
       case 16: return run_fwd_d<float, 16>(id, p, causal, st);
@@ -755,7 +765,7 @@ int launch_fwd(const FwdParams& p, int D, int dtype, bool causal, int id, hipStr
 }
 
 int fwd_lds_bytes(int D, int dtype, const TileEntry& e) {
-  if (dtype == 0) {
+  if (dtype == 0 || dtype == 2) {
     switch (D) {
       case 16: return PipeLayout<16>::LDS;
       case 32: return PipeLayout<32>::LDS;
@@ -763,7 +773,7 @@ int fwd_lds_bytes(int D, int dtype, const TileEntry& e) {
       case 128: return PipeLayout<128>::LDS;
     }
   }
-  const int sz = dtype == 0 ? 2 : 4;
+  const int sz = dtype == 1 ? 4 : 2;
   const int rk = D * sz + 16, rv = D * sz + (sz == 2 ? 32 : 16);
   return 2 * e.other * (rk + rv);
 }

@@ -19,7 +19,7 @@ struct TileEntry {
   int tiles;  // 32-row MFMA tiles per wave (queries for fwd/dQ, keys for dK/dV)
   int other;  // keys per step (fwd, dQ) or queries per step (dK/dV)
   int occ;    // waves per SIMD the kernel is compiled for (register budget 512 / occ)
-  int pipe;   // 1: software-pipelined fp16 kernel, 0: generic kernel
+  int pipe;   // 1: software-pipelined 16-bit kernel, 0: generic kernel
 };
 
 // ---- forward ----------------------------------------------------------------------------
@@ -29,13 +29,17 @@ template <typename T, int D> struct FwdTable;
     static constexpr TileEntry e[] = {__VA_ARGS__};                     \
     static constexpr int n = sizeof(e) / sizeof(e[0]);                  \
   };
+// The 16-bit element types (fp16, bf16) share one table: same kernels, same tiles.
+#define TATTN_TABLE16(NAME, D, ...)          \
+  TATTN_TABLE(NAME, _Float16, D, __VA_ARGS__) \
+  TATTN_TABLE(NAME, __bf16, D, __VA_ARGS__)
 
-// Entry 0 of each table is the default pick. fp16 forward entries and the fp16 backward
+// Entry 0 of each table is the default pick. 16-bit forward entries and the 16-bit backward
 // entries marked pipe run the software-pipelined kernels (32 rows per step).
-TATTN_TABLE(FwdTable, _Float16, 16, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1})
-TATTN_TABLE(FwdTable, _Float16, 32, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1})
-TATTN_TABLE(FwdTable, _Float16, 64, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1}, {8, 2, 32, 2, 1}, {4, 1, 32, 4, 1})
-TATTN_TABLE(FwdTable, _Float16, 128, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 1, 1})
+TATTN_TABLE16(FwdTable, 16, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1})
+TATTN_TABLE16(FwdTable, 32, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1})
+TATTN_TABLE16(FwdTable, 64, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1}, {8, 2, 32, 2, 1}, {4, 1, 32, 4, 1})
+TATTN_TABLE16(FwdTable, 128, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 1, 1})
 TATTN_TABLE(FwdTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(FwdTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(FwdTable, float, 64, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
@@ -47,10 +51,10 @@ namespace tattn {
 
 // ---- backward dK/dV: {waves, key tiles per wave, queries per step} -------------------------
 template <typename T, int D> struct DkdvTable;
-TATTN_TABLE(DkdvTable, _Float16, 16, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {4, 2, 32, 2, 0})
-TATTN_TABLE(DkdvTable, _Float16, 32, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {4, 2, 32, 2, 0})
-TATTN_TABLE(DkdvTable, _Float16, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {8, 1, 64, 2, 0}, {4, 2, 32, 2, 0})
-TATTN_TABLE(DkdvTable, _Float16, 128, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
+TATTN_TABLE16(DkdvTable, 16, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {4, 2, 32, 2, 0})
+TATTN_TABLE16(DkdvTable, 32, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {4, 2, 32, 2, 0})
+TATTN_TABLE16(DkdvTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {8, 1, 64, 2, 0}, {4, 2, 32, 2, 0})
+TATTN_TABLE16(DkdvTable, 128, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DkdvTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DkdvTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DkdvTable, float, 64, {4, 1, 32, 2, 0})
@@ -58,10 +62,10 @@ TATTN_TABLE(DkdvTable, float, 128, {4, 1, 32, 2, 0})
 
 // ---- backward dQ: {waves, query tiles per wave, keys per step} ------------------------------
 template <typename T, int D> struct DqTable;
-TATTN_TABLE(DqTable, _Float16, 16, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0})
-TATTN_TABLE(DqTable, _Float16, 32, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0})
-TATTN_TABLE(DqTable, _Float16, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {8, 1, 64, 2, 0})
-TATTN_TABLE(DqTable, _Float16, 128, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
+TATTN_TABLE16(DqTable, 16, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0})
+TATTN_TABLE16(DqTable, 32, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0})
+TATTN_TABLE16(DqTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {8, 1, 64, 2, 0})
+TATTN_TABLE16(DqTable, 128, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DqTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DqTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DqTable, float, 64, {4, 1, 32, 2, 0})

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported before the library is loaded, see 
 LIB_PATH = Path(__file__).resolve().with_name("libtattn_hip.so")
 ABI_VERSION = 1
 
-F16, F32 = 0, 1
+F16, F32, BF16 = 0, 1, 2
 K_FWD, K_BWD_DKDV, K_BWD_DQ = 0, 1, 2
 KERNEL_NAMES = {K_FWD: "fwd", K_BWD_DKDV: "bwd_dkdv", K_BWD_DQ: "bwd_dq"}
 

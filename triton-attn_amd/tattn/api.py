@@ -21,7 +21,7 @@ from tattn import _lib
 
 Config = Union[int, dict, None]
 
-_DTYPES = {torch.float16: _lib.F16, torch.float32: _lib.F32}
+_DTYPES = {torch.float16: _lib.F16, torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
 
 
 def hip_available(device: torch.device) -> bool:
@@ -54,8 +54,11 @@ def _check(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
     d = q.shape[-1]
     if d not in (16, 32, 64, 128):
         raise ValueError(f"head dim must be 16, 32, 64 or 128, got {d}")
-    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.float16, torch.float32):
-        raise ValueError(f"q, k, v must share dtype float16 or float32, got {q.dtype}, {k.dtype}, {v.dtype}")
+    # bfloat16 is accepted in addition to the reference's float16 / float32 (api.py:55-56).
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _DTYPES:
+        raise ValueError(
+            f"q, k, v must share dtype float16, bfloat16 or float32, got {q.dtype}, {k.dtype}, {v.dtype}"
+        )
 
 
 def _bucket(n: int) -> int:

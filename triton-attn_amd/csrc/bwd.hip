@@ -164,7 +164,8 @@ __global__ __launch_bounds__(NW * 64, 2) void dkdv_kernel(const BwdParams p) {
   const int lane = tid & 63, w = tid >> 6, h2 = lane >> 5, l32 = lane & 31;
   const int N = p.N;
   const int zhs = p.Z * p.H;
-  const int zh = blockIdx.x % zhs, kblk_i = blockIdx.x / zhs;  // small key blocks (most work) first
+  const BlockCoord bc = block_coord(zhs, p.n_blocks, !CAUSAL);
+  const int zh = bc.zh, kblk_i = bc.blk;  // causal: small key blocks (most work) first
   const Head hd = head_of(p, zh);
   const T* Qg = (const T*)p.q + hd.off;
   const T* Kg = (const T*)p.k + hd.off;
@@ -390,8 +391,9 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_kernel(const BwdParams p) {
   const int lane = tid & 63, w = tid >> 6, h2 = lane >> 5, l32 = lane & 31;
   const int N = p.N;
   const int zhs = p.Z * p.H;
-  const int zh = blockIdx.x % zhs;
-  int qb = blockIdx.x / zhs;
+  const BlockCoord bc = block_coord(zhs, p.n_blocks, !CAUSAL);
+  const int zh = bc.zh;
+  int qb = bc.blk;
   if (CAUSAL) qb = p.n_blocks - 1 - qb;  // longest rows first
   const Head hd = head_of(p, zh);
   const T* Qg = (const T*)p.q + hd.off;

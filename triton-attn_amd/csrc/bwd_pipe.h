@@ -80,7 +80,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
   const int lane = tid & 63, w = tid >> 6, h2 = lane >> 5, l32 = lane & 31;
   const int N = p.N;
   const int zhs = p.Z * p.H;
-  const int zh = blockIdx.x % zhs, kbi = blockIdx.x / zhs;  // small key blocks (most work) first
+  const BlockCoord bc = block_coord(zhs, p.n_blocks, !CAUSAL);
+  const int zh = bc.zh, kbi = bc.blk;  // causal: small key blocks (most work) first
   const int64_t hoff = (int64_t)(zh / p.H) * p.s[0] + (int64_t)(zh % p.H) * p.s[1];
   const int64_t rs = p.s[2];
   const float c = p.c;
@@ -315,8 +316,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
   const int lane = tid & 63, w = tid >> 6, h2 = lane >> 5, l32 = lane & 31;
   const int N = p.N;
   const int zhs = p.Z * p.H;
-  const int zh = blockIdx.x % zhs;
-  int qb = blockIdx.x / zhs;
+  const BlockCoord bc = block_coord(zhs, p.n_blocks, !CAUSAL);
+  const int zh = bc.zh;
+  int qb = bc.blk;
   if (CAUSAL) qb = p.n_blocks - 1 - qb;  // longest rows first
   const int64_t hoff = (int64_t)(zh / p.H) * p.s[0] + (int64_t)(zh % p.H) * p.s[1];
   const int64_t rs = p.s[2];

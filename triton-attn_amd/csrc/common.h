@@ -197,6 +197,25 @@ __device__ __forceinline__ u32x4 rsrc_load(__amdgpu_buffer_rsrc_t r, uint32_t of
 }
 
 
+// Workgroup -> (z*H + h slice, block within the slice). Workgroups are dispatched round-robin over
+// the 8 XCDs, so workgroup b runs on XCD b % 8, and each XCD has its own L2. Both orders keep a
+// slice on one XCD when Z*H is a multiple of 8. grouped: the workgroups of an XCD take every block
+// of one slice before the next slice, so the blocks that stream the same K/V (or Q/dO) rows run
+// together and share them through that L2. Otherwise consecutive workgroups take consecutive
+// slices and the blocks of a slice come one dispatch round apart, which keeps an order over block
+// indices (the causal kernels' longest-first) global across the launch.
+struct BlockCoord {
+  int zh, blk;
+};
+__device__ __forceinline__ BlockCoord block_coord(int zhs, int nblk, bool grouped) {
+  const int b = blockIdx.x;
+  if (grouped && (zhs & 7) == 0) {
+    const int l = b >> 3;
+    return {(l / nblk) * 8 + (b & 7), l % nblk};
+  }
+  return {b % zhs, b / zhs};
+}
+
 // fp16 tiles are stored without padding, with the 16-byte chunks of row r XOR-permuted by
 // swz(r). The permutation is chosen so that both access patterns of these tiles hit 64
 // distinct banks per 256 bytes: 16 consecutive rows read at one chunk (natural MFMA operands,

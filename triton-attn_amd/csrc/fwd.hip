@@ -64,8 +64,9 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_generic_kernel(const FwdParams
   const int lane = tid & 63, w = tid >> 6, h2 = lane >> 5, l32 = lane & 31;
   const int N = p.N;
   const int zhs = p.Z * p.H;
-  const int zh = blockIdx.x % zhs;
-  int qb = blockIdx.x / zhs;
+  const BlockCoord bc = block_coord(zhs, p.n_qblocks, !CAUSAL);
+  const int zh = bc.zh;
+  int qb = bc.blk;
   if (CAUSAL) qb = p.n_qblocks - 1 - qb;  // longest rows first
   const int64_t z = zh / p.H, hh = zh % p.H;
   const T* Q = (const T*)p.q + z * p.sq[0] + hh * p.sq[1];
@@ -359,8 +360,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   const int lane = tid & 63, w = tid >> 6, h2 = lane >> 5, l32 = lane & 31;
   const int N = p.N;
   const int zhs = p.Z * p.H;
-  const int zh = blockIdx.x % zhs;
-  int qb = blockIdx.x / zhs;
+  const BlockCoord bc = block_coord(zhs, p.n_qblocks, !CAUSAL);
+  const int zh = bc.zh;
+  int qb = bc.blk;
   if (CAUSAL) qb = p.n_qblocks - 1 - qb;  // longest rows first
   const int64_t z = zh / p.H, hh = zh % p.H;
   const T* Q = (const T*)p.q + z * p.sq[0] + hh * p.sq[1];

@@ -107,8 +107,10 @@ int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N) {
   switch (kernel) {
     case TATTN_K_FWD:  // short rows: 128-row blocks; long: 256 rows (causal) or 512 rows
       if (causal) return N >= 8192 ? 0 : 1;
-      return N >= 8192 ? 3 : N >= 2048 ? 0 : 1;
+      return N >= 8192 ? 3 : N >= 1024 ? 0 : 1;
     case TATTN_K_BWD_DKDV:  // pipelined, 4 waves (128 keys) or 8 waves (256 keys)
+      if (!causal) return 1;
+      return N >= 2048 ? 1 : 0;
     case TATTN_K_BWD_DQ:
       return N >= 2048 ? 1 : 0;
   }

@@ -158,15 +158,24 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
         st16(base + ldst[i], pq[i]);
         st16(base + B::TILE + ldst[i], pd[i]);
       }
-    if (md_loader) *reinterpret_cast<uint32_t*>(base + md_dst) = (tid & 32) ? pdl : pm;
+    // delta is staged negated: it seeds the dP accumulator, so dP - delta comes out of the MFMAs.
+    if (md_loader) *reinterpret_cast<uint32_t*>(base + md_dst) = (tid & 32) ? (pdl ^ 0x80000000u) : pm;
   };
 
-  // S = Q K^T and dP = dO V^T of the stage's 32 queries (C layout: lane = key,
-  // register r = query kappa(r, h2)).
+  // S = Q K^T and dP - delta = dO V^T - delta of the stage's 32 queries (C layout: lane = key,
+  // register r = query kappa(r, h2)); the dP chain starts from the stage's -delta.
   auto qk = [&](f32x16& s, f32x16& dp, int st) {
     const char* base = smem + st * STAGE;
     s = f32x16{};
-    dp = f32x16{};
+    {
+      const TATTN_LDS char* nd = (const TATTN_LDS char*)base + mo + 128;
+      const f32x4 n0 = *reinterpret_cast<const TATTN_LDS f32x4*>(nd);
+      const f32x4 n1 = *reinterpret_cast<const TATTN_LDS f32x4*>(nd + 16);
+      const f32x4 n2 = *reinterpret_cast<const TATTN_LDS f32x4*>(nd + 64);
+      const f32x4 n3 = *reinterpret_cast<const TATTN_LDS f32x4*>(nd + 80);
+      dp = f32x16{n0[0], n0[1], n0[2], n0[3], n1[0], n1[1], n1[2], n1[3],
+                  n2[0], n2[1], n2[2], n2[3], n3[0], n3[1], n3[2], n3[3]};
+    }
 #pragma unroll
     for (int sd = 0; sd < NSD; ++sd) {
       s = Elt<T>::mfma(lds8<T>(base + nat[sd]), kop[sd], s);
@@ -187,7 +196,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
         dk[u] = Elt<T>::mfma(dsp[sl], qb, dk[u]);
       }
   };
-  // P = exp2(S c - M), dS = P (dP - delta) for the stage's queries, rounded into MFMA operands.
+  // P = exp2(S c - M), dS = P (dP - delta) for the stage's queries, rounded into MFMA operands
+  // (dp already holds dP - delta).
   auto pds = [&](const f32x16& s, const f32x16& dp, V8* pp, V8* dsp, int st, int q0, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const char* base = smem + st * STAGE;
@@ -196,8 +206,6 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
     for (int a = 0; a < 2; ++a) {
       const f32x4 m0 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 64 * a);
       const f32x4 m1 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 64 * a + 16);
-      const f32x4 d0 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 128 + 64 * a);
-      const f32x4 d1 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 128 + 64 * a + 16);
       V8 x, y;
 #pragma unroll
       for (int i = 0; i < 8; i += 2) {
@@ -206,11 +214,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
         for (int e = 0; e < 2; ++e) {
           const int r = 8 * a + i + e;
           const float mv = (i + e) < 4 ? m0[i + e] : m1[i + e - 4];
-          const float dl = (i + e) < 4 ? d0[i + e] : d1[i + e - 4];
           float pv = fast_exp2(__builtin_fmaf(s[r], c, -mv));
           if constexpr (MASK) pv = key > q0 + kappa(r, h2) ? 0.0f : pv;
           pr[e] = pv;
-          dr[e] = pv * (dp[r] - dl);
+          dr[e] = pv * dp[r];
         }
         const V2 ph = H::pack(pr[0], pr[1]), dh = H::pack(dr[0], dr[1]);
         x[i] = ph[0];
@@ -340,6 +347,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
   }
   const float nm = -(q < N ? p.m[(int64_t)zh * N + q] : 0.0f);
   const float dl = q < N ? p.delta[(int64_t)zh * N + q] : 0.0f;
+  // -delta of the lane's query in every register: seeds the dP^T accumulator, so the MFMAs
+  // return dP - delta.
+  f32x16 ndl;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) ndl[r] = -dl;
   f32x16 dq[DT];
 #pragma unroll
   for (int u = 0; u < DT; ++u) dq[u] = f32x16{};
@@ -390,12 +402,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
         st16(base + B::TILE + ldst[i], pv[i]);
       }
   };
-  // S^T = K Q^T and dP^T = V dO^T of the stage's 32 keys (C layout: lane = query,
+  // S^T = K Q^T and dP^T - delta = V dO^T - delta of the stage's 32 keys (C layout: lane = query,
   // register r = key kappa(r, h2)).
   auto qk = [&](f32x16& s, f32x16& dp, int st) {
     const char* base = smem + st * STAGE;
     s = f32x16{};
-    dp = f32x16{};
+    dp = ndl;
 #pragma unroll
     for (int sd = 0; sd < NSD; ++sd) {
       s = Elt<T>::mfma(lds8<T>(base + nat[sd]), qop[sd], s);
@@ -430,7 +442,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
             const int key = kb + kappa(r, h2);
             pv2 = (key >= N || (CAUSAL && key > q)) ? 0.0f : pv2;
           }
-          dr[e] = pv2 * (dp[r] - dl);
+          dr[e] = pv2 * dp[r];
         }
         const V2 dh = H::pack(dr[0], dr[1]);
         x[i] = dh[0];

@@ -196,6 +196,24 @@ def counter_means(dirs: list[str]) -> dict[str, dict[str, float]]:
     return {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in acc.items()}
 
 
+def derived(cs: dict[str, float]) -> dict[str, float]:
+    """Ratios from counter means (each present only when its counters were collected):
+    mfma_busy: MFMA-busy SIMD cycles per SIMD cycle of the CUs' busy time (4 SIMDs per CU);
+    lds_bank_conflict_per_lds_cycle: bank-conflict cycles per cycle with an LDS instruction active;
+    valu_per_mfma: VALU instructions per MFMA instruction;
+    lds_load_bytes: LDS read bytes (SQ_INSTS_LDS_LOAD_BANDWIDTH counts 64-byte units)."""
+    out: dict[str, float] = {}
+    if cs.get("SQ_BUSY_CU_CYCLES") and "SQ_VALU_MFMA_BUSY_CYCLES" in cs:
+        out["mfma_busy"] = cs["SQ_VALU_MFMA_BUSY_CYCLES"] / (4 * cs["SQ_BUSY_CU_CYCLES"])
+    if cs.get("SQ_ACTIVE_INST_LDS") and "SQ_LDS_BANK_CONFLICT" in cs:
+        out["lds_bank_conflict_per_lds_cycle"] = cs["SQ_LDS_BANK_CONFLICT"] / cs["SQ_ACTIVE_INST_LDS"]
+    if cs.get("SQ_INSTS_MFMA") and "SQ_INSTS_VALU" in cs:
+        out["valu_per_mfma"] = cs["SQ_INSTS_VALU"] / cs["SQ_INSTS_MFMA"]
+    if "SQ_INSTS_LDS_LOAD_BANDWIDTH" in cs:
+        out["lds_load_bytes"] = cs["SQ_INSTS_LDS_LOAD_BANDWIDTH"] * 64
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--sources", default="fwd.hip,bwd.hip", help="kernel sources under csrc/")
@@ -204,7 +222,9 @@ def main() -> int:
     ap.add_argument("--out", default=None, help="write the JSON result here")
     a = ap.parse_args()
     if a.counters:
-        res: dict[str, Any] = {"counters": counter_means(a.counters)}
+        means = counter_means(a.counters)
+        names = _demangle(list(means))
+        res: dict[str, Any] = {"counters": {names[k]: {**cs, "derived": derived(cs)} for k, cs in means.items()}}
     else:
         res = {"arch": "gfx950", "kernels": {}}
         for src in a.sources.split(","):

@@ -1,0 +1,114 @@
+"""The benchmark workloads and the edge-shape sweep at their real sizes, checked against float32
+materialised attention and its autograd on the same seeded inputs.
+
+- Edge shapes: head dims 16/32/64, sequence lengths 1/17/33/70 (not multiples of any tile),
+  batch 2, heads 3, q/k/v/dO made non-contiguous by transposing a [B, N, H, D] tensor to
+  [B, H, N, D]; fp16 and fp32, causal and not; output and all three gradients.
+- Full size: fp16, H=16, D=64, B x N = 16,384 tokens at every N from 512 to 16,384, causal
+  and not, N(0,1) inputs; output and dq/dk/dv.
+- Long context: B=1, H=16, N=16,384, D=64, inputs scaled by 0.5, causal and not; output and
+  gradients, and the extra memory of forward + backward beyond inputs, outputs and gradients.
+
+Tolerances: fp16 |err| <= 2e-3 + 2e-3 |ref| (output and gradients), fp32 1e-5 + 1e-5 |ref|.
+The float32 reference is computed a few heads at a time so its N x N matrices stay near 1 GiB."""
+
+import pytest
+import torch
+
+from helpers import rand
+from oracle.reference import naive_attention
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+F16_TOL = {"atol": 2e-3, "rtol": 2e-3}
+F32_TOL = {"atol": 1e-5, "rtol": 1e-5}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from tattn import hip_available
+
+    assert hip_available(DEV), "libtattn_hip.so did not load or the device is not a gfx950"
+
+
+def _reference(q, k, v, do, causal):
+    """float32 output and gradients, computed over chunks of (batch, head) pairs."""
+    z, h, n, d = q.shape
+    per = max(1, (1 << 28) // (n * n))  # (batch, head) pairs per chunk: ~1 GiB of scores
+    outs = [torch.empty((z, h, n, d), device=q.device, dtype=torch.float32) for _ in range(4)]
+    flat = [t.reshape(z * h, 1, n, d) for t in (q, k, v, do)]
+    for s in range(0, z * h, per):
+        e = min(z * h, s + per)
+        qc, kc, vc = (t[s:e].transpose(0, 1).float().contiguous().requires_grad_() for t in flat[:3])
+        dc = flat[3][s:e].transpose(0, 1).float().contiguous()
+        o = naive_attention(qc, kc, vc, causal=causal)
+        o.backward(dc)
+        for dst, src in zip(outs, (o.detach(), qc.grad, kc.grad, vc.grad)):
+            dst.reshape(z * h, n, d)[s:e] = src[0]
+    return outs
+
+
+def _run(q, k, v, do, causal):
+    from tattn import attention
+
+    qs, ks, vs = (t.detach().clone().requires_grad_() for t in (q, k, v))
+    o = attention(qs, ks, vs, causal=causal)
+    o.backward(do)
+    return [o.detach().float(), qs.grad.float(), ks.grad.float(), vs.grad.float()]
+
+
+@pytest.mark.parametrize("d", [16, 32, 64])
+@pytest.mark.parametrize("n", [1, 17, 33, 70])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_edge_shapes_noncontiguous(d, n, causal, dtype):
+    seed = 1000 * d + 10 * n + int(causal)
+    q, k, v, do = (rand((2, n, 3, d), dtype, seed + i, DEV).transpose(1, 2) for i in range(4))
+    assert not q.is_contiguous() or n == 1
+    got = _run(q, k, v, do, causal)
+    want = _reference(q, k, v, do, causal)
+    tol = F16_TOL if dtype == torch.float16 else F32_TOL
+    for name, g, w in zip(("o", "dq", "dk", "dv"), got, want):
+        torch.testing.assert_close(g, w, **tol, msg=lambda m: f"{name} d={d} n={n} causal={causal}: {m}")
+
+
+@pytest.mark.parametrize("n", [512, 1024, 2048, 4096, 8192, 16384])
+@pytest.mark.parametrize("causal", [False, True])
+def test_full_size_fp16(n, causal):
+    b = 16384 // n
+    g = torch.Generator(device=DEV).manual_seed(n + int(causal))
+    q, k, v, do = (torch.randn(b, 16, n, 64, device=DEV, dtype=torch.float16, generator=g) for _ in range(4))
+    got = _run(q, k, v, do, causal)
+    want = _reference(q, k, v, do, causal)
+    for name, gt, w in zip(("o", "dq", "dk", "dv"), got, want):
+        torch.testing.assert_close(gt, w, **F16_TOL, msg=lambda m: f"{name} n={n} causal={causal}: {m}")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_long_context_scaled_inputs_and_memory(causal):
+    from tattn import attention
+
+    g = torch.Generator(device=DEV).manual_seed(77 + int(causal))
+    q, k, v, do = (0.5 * torch.randn(1, 16, 16384, 64, device=DEV, dtype=torch.float16, generator=g)
+                   for _ in range(4))
+    got = _run(q, k, v, do, causal)
+    want = _reference(q, k, v, do, causal)
+    for name, gt, w in zip(("o", "dq", "dk", "dv"), got, want):
+        torch.testing.assert_close(gt, w, **F16_TOL, msg=lambda m: f"{name} causal={causal}: {m}")
+    del got, want
+
+    # Extra memory of forward + backward: M (saved), delta and the fp32 workspace of nothing
+    # else. Inputs, output, dO and the three gradients are excluded.
+    qs, ks, vs = (t.detach().clone().requires_grad_() for t in (q, k, v))
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(DEV)
+    base = torch.cuda.memory_allocated(DEV)
+    o = attention(qs, ks, vs, causal=causal)
+    o.backward(do)
+    torch.cuda.synchronize()
+    extra = torch.cuda.max_memory_allocated(DEV) - base - 4 * q.numel() * q.element_size()
+    # M and delta: 2 x [1, 16, 16384] float32 = 2 MiB.
+    assert extra <= 2 * 16 * 16384 * 4 + (1 << 20), f"extra memory {extra / 2**20:.1f} MiB"

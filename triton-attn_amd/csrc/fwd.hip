@@ -531,42 +531,75 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
     }
     return any_upd;
   };
-  auto rescale = [&](bool any_upd, const float* alpha) {
-    if (__builtin_amdgcn_ballot_w64(any_upd)) {
-#pragma unroll
-      for (int j = 0; j < QT; ++j)
-#pragma unroll
-        for (int u = 0; u < DT; ++u) acc[u][j] *= alpha[j];
-    }
-  };
   // Unmasked steps: probabilities with the running max as it stands (no row max), summed with
   // v_dot2 (fast_probs). A lane whose 16 probabilities sum above 2^12 (some score exceeds the
   // max used in the exponent by more than 12 in base 2; an unset max gives +inf) sends the
   // wave down the slow path (fast_fixup): row max, lazy update, accumulator rescale,
   // probabilities recomputed. Probabilities fed to the MFMAs therefore stay at or below 2^12,
   // far inside fp16, and rows whose max moves by less than that skip the max entirely.
+  // Diagonal 32x32 tile (first key = first row): register r of the lane holds key offset
+  // kappa(r, h2) of row offset l32; keys past the row are hidden.
+  bool diag_hide[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) diag_hide[r] = CAUSAL && kappa(r, h2) > l32;
+  // Probabilities of one 32x32 tile with the row max as it stands; with MASK, keys whose hide[r]
+  // is set get probability 0 (applied after the exponential, so no inf - inf arises).
+  auto tile_probs = [&](const f32x16& st, V8* pt, float nm, const bool* hide, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    float acc_s = 0.0f;
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg) {
+      V8 x;
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        float e0 = fast_exp2(__builtin_fmaf(st[8 * sg + i], c, nm));
+        float e1 = fast_exp2(__builtin_fmaf(st[8 * sg + i + 1], c, nm));
+        if constexpr (MASK) {
+          e0 = hide[8 * sg + i] ? 0.0f : e0;
+          e1 = hide[8 * sg + i + 1] ? 0.0f : e1;
+        }
+        const V2 pr = H::pack(e0, e1);
+        acc_s = H::sum2(pr, acc_s);
+        x[i] = pr[0];
+        x[i + 1] = pr[1];
+      }
+      pt[sg] = x;
+    }
+    return acc_s;
+  };
   auto fast_probs = [&](f32x16* scur, V8 (*pc)[2], float* ps) {
     bool need = false;
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
-      const float nm = -mrow[j];
-      float acc_s = 0.0f;
+      ps[j] = tile_probs(scur[j], pc[j], -mrow[j], nullptr, std::false_type{});
+      need |= !(ps[j] <= 4096.0f);
+    }
+    return need;
+  };
+  // Steps that need a mask (keys past the sequence end, or causal steps across the workgroup's
+  // diagonal) take the same fast path per 32x32 tile, by the tile's place against the diagonal
+  // (wave-uniform): keys all at or below its rows: as is; keys all above: probabilities zero, no
+  // exponentials; on the diagonal (first row = first key): keys past the row hidden with the
+  // fixed lane pattern diag_hide (key offset kappa(r, h2) > row offset l32). In the step holding
+  // the sequence end, key offsets N - 32i and beyond are hidden as well. Hidden keys get
+  // probability 0. An unset max (-inf, first visible keys of a row) gives an inf sum and so the
+  // slow path, which masks in full.
+  auto mask_probs = [&](f32x16* scur, V8 (*pc)[2], float* ps, int i) {
+    bool need = false;
+    const int kend = N - 32 * i - 8 * h2;  // register r is past the end if 16(r/8) + r%8 >= kend
 #pragma unroll
-      for (int sg = 0; sg < 2; ++sg) {
-        V8 x;
-#pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-          const float e0 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i], c, nm));
-          const float e1 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i + 1], c, nm));
-          const V2 pr = H::pack(e0, e1);
-          acc_s = H::sum2(pr, acc_s);
-          x[i] = pr[0];
-          x[i + 1] = pr[1];
-        }
-        pc[j][sg] = x;
+    for (int j = 0; j < QT; ++j) {
+      const int rel = CAUSAL ? qw0 + 32 * j - 32 * i : 32;
+      if (rel < 0) {
+        pc[j][0] = pc[j][1] = V8{};
+        ps[j] = 0.0f;
+        continue;
       }
-      ps[j] = acc_s;
-      need |= !(acc_s <= 4096.0f);
+      bool hide[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) hide[r] = (rel == 0 && diag_hide[r]) || 16 * (r >> 3) + (r & 7) >= kend;
+      ps[j] = tile_probs(scur[j], pc[j], -mrow[j], hide, std::true_type{});
+      need |= !(ps[j] <= 4096.0f);
     }
     return need;
   };
@@ -574,7 +607,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   // need not stay live through the fast path. The slow path is the body of a one-sided branch
   // (the fast path's state updates come first and are undone there): a two-sided branch that
   // updates the accumulators on one side only makes the register allocator double them.
-  auto fast_fixup = [&](bool need, f32x16* scur, V8 (*pc)[2], const float* ps, int kc_) {
+  auto fast_fixup = [&](bool need, f32x16* scur, V8 (*pc)[2], const float* ps, int kc_, int kb,
+                        auto mask_tag) {
     float lprev[QT];
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
@@ -586,7 +620,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
       for (int j = 0; j < QT; ++j) lrow[j] = lprev[j];
       qk(scur, kc_);
       float alpha[QT];
-      (void)softmax(scur, pc, alpha, 0, std::false_type{});
+      (void)softmax(scur, pc, alpha, kb, mask_tag);
 #pragma unroll
       for (int j = 0; j < QT; ++j)
 #pragma unroll
@@ -627,7 +661,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
     qk(snext, (IV + 1) % 4);
     float ps[QT];
     const bool need = fast_probs(scur, pcur, ps);
-    fast_fixup(need, scur, pcur, ps, IV);
+    fast_fixup(need, scur, pcur, ps, IV, 0, std::false_type{});
     step_end();
   };
 
@@ -644,15 +678,16 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
     if (i - 1 < wave_steps) pv_mma(pa, (i + 3) & 3);
     if (i < wave_steps) {
       qk(sb, (i + 1) & 3);
-      float alpha[QT];
-      if (i >= n_full) {
-        const bool upd = softmax(sa, pb, alpha, 32 * i, std::true_type{});
-        rescale(upd, alpha);
+      float ps[QT];
+      bool need;
+      if (i == 0) {  // no max yet: straight to the (masked) softmax
+        need = true;
+#pragma unroll
+        for (int j = 0; j < QT; ++j) ps[j] = 0.0f;
       } else {
-        float ps[QT];
-        const bool need = fast_probs(sa, pb, ps);
-        fast_fixup(need, sa, pb, ps, i & 3);
+        need = i >= n_full ? mask_probs(sa, pb, ps, i) : fast_probs(sa, pb, ps);
       }
+      fast_fixup(need, sa, pb, ps, i & 3, 32 * i, std::true_type{});
 #pragma unroll
       for (int j = 0; j < QT; ++j) {
         sa[j] = sb[j];

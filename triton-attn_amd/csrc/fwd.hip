@@ -533,8 +533,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   };
   // Unmasked steps: probabilities with the running max as it stands (no row max), summed with
   // v_dot2 (fast_probs). A lane whose 16 probabilities sum above 2^12 (some score exceeds the
-  // max used in the exponent by more than 12 in base 2; an unset max gives +inf) sends the
-  // wave down the slow path (fast_fixup): row max, lazy update, accumulator rescale,
+  // max used in the exponent by more than 12 in base 2) sends the wave down the slow path (fast_fixup): row max, lazy update, accumulator rescale,
   // probabilities recomputed. Probabilities fed to the MFMAs therefore stay at or below 2^12,
   // far inside fp16, and rows whose max moves by less than that skip the max entirely.
   // Diagonal 32x32 tile (first key = first row): register r of the lane holds key offset
@@ -582,8 +581,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   // exponentials; on the diagonal (first row = first key): keys past the row hidden with the
   // fixed lane pattern diag_hide (key offset kappa(r, h2) > row offset l32). In the step holding
   // the sequence end, key offsets N - 32i and beyond are hidden as well. Hidden keys get
-  // probability 0. An unset max (-inf, first visible keys of a row) gives an inf sum and so the
-  // slow path, which masks in full.
+  // probability 0, set after the exponential (no inf - inf); the slow path masks in full.
   auto mask_probs = [&](f32x16* scur, V8 (*pc)[2], float* ps, int i) {
     bool need = false;
     const int kend = N - 32 * i - 8 * h2;  // register r is past the end if 16(r/8) + r%8 >= kend
@@ -628,8 +626,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
     }
   };
 
-  // Prologue: K_0..K_2 and V_0..V_2 into slots 0..2; V slot 3 (read by step 0 together with
-  // all-zero probabilities) cleared.
+  // Prologue: K_0..K_2 and V_0..V_2 into slots 0..2; V slot 3 (read by a full step 0 together
+  // with all-zero probabilities) cleared.
   dma(0, 0, 0, 0);
   dma(1, 1, 1, 1);
   dma(2, 2, 2, 2);
@@ -640,7 +638,22 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   V8 pa[QT][2], pb[QT][2];
 #pragma unroll
   for (int j = 0; j < QT; ++j) pa[j][0] = pa[j][1] = V8{};
-  if (wave_steps > 0) qk(sa, 0);
+  if (wave_steps > 0) {
+    qk(sa, 0);
+    // Running max seeded with step 0's row max over its visible keys (what the slow path would
+    // set there), so step 0 takes the fast path like any other step.
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
+      const int q = qw0 + 32 * j + l32;
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kappa(r, h2);
+        mx = (key < N && (!CAUSAL || key <= q)) ? __builtin_fmaxf(mx, sa[j][r]) : mx;
+      }
+      mrow[j] = max_halves(mx) * c;
+    }
+  }
 
   // Steps before n_full need no mask for any wave of the workgroup (all keys below the
   // workgroup's first query row and inside the sequence): they run four per trip so ring
@@ -675,18 +688,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   // Remaining steps (masked or not) with run-time slots; state: scur = sa, pprev = pa.
   for (; i < nsteps; ++i) {
     dma(i + 3, i + 1, (i + 3) & 3, (i + 1) & 3);
-    if (i - 1 < wave_steps) pv_mma(pa, (i + 3) & 3);
+    if (i > 0 && i - 1 < wave_steps) pv_mma(pa, (i + 3) & 3);
     if (i < wave_steps) {
       qk(sb, (i + 1) & 3);
       float ps[QT];
-      bool need;
-      if (i == 0) {  // no max yet: straight to the (masked) softmax
-        need = true;
-#pragma unroll
-        for (int j = 0; j < QT; ++j) ps[j] = 0.0f;
-      } else {
-        need = i >= n_full ? mask_probs(sa, pb, ps, i) : fast_probs(sa, pb, ps);
-      }
+      const bool need = i >= n_full ? mask_probs(sa, pb, ps, i) : fast_probs(sa, pb, ps);
       fast_fixup(need, sa, pb, ps, i & 3, 32 * i, std::true_type{});
 #pragma unroll
       for (int j = 0; j < QT; ++j) {

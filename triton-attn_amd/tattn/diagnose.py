@@ -154,17 +154,31 @@ def isa_stats(asm: str, name_filter: str = "") -> dict[str, dict[str, Any]]:
             if mm and mm.group(1) in _INFO_KEYS:
                 info[_INFO_KEYS[mm.group(1)]] = int(mm.group(2))
             k += 1
-        # Main loop: of the loops (header label to the last branch back to it), the one with the
-        # most MFMAs.
+        # Main loop: the loop with the most MFMAs. Loop membership comes from the compiler's block
+        # notes: a header block says "Loop Header", every other block of a loop says
+        # "in Loop: Header=BBx_y" (its innermost loop); a loop's lines are its header block and
+        # the blocks whose innermost loop it is.
+        blocks: list[tuple[str | None, list[str]]] = []  # (innermost loop header, lines)
+        for line in body:
+            m_lab = re.match(r"^\.L(BB\d+_\d+):", line)
+            if m_lab or re.match(r"^; %bb\.\d+:", line):
+                m_in = re.search(r"in Loop: Header=(BB\d+_\d+)", line)
+                own = m_lab.group(1) if m_lab and "Loop Header" in line else None
+                blocks.append((own or (m_in.group(1) if m_in else None), [line]))
+            elif blocks:
+                if "Loop Header" in line and blocks[-1][1][0].startswith(".L"):  # note on the next line
+                    lab = re.match(r"^\.L(BB\d+_\d+):", blocks[-1][1][0])
+                    blocks[-1] = (lab.group(1) if lab else blocks[-1][0], blocks[-1][1])
+                blocks[-1][1].append(line)
+        loops: dict[str, list[str]] = collections.defaultdict(list)
+        for head, lines_ in blocks:
+            if head:
+                loops[head].extend(lines_)
         main_loop = None
-        for st in (n for n, line in enumerate(body) if "Loop Header" in line):
-            head = body[st].split(":")[0].strip()
-            back = [n for n, line in enumerate(body)
-                    if re.match(r"^\s*s_(?:cbranch_\w+|branch)\s+" + re.escape(head) + r"\b", line)]
-            if back:
-                c = _counts(body[st:back[-1] + 1])
-                if main_loop is None or c["mfma"] > main_loop["mfma"]:
-                    main_loop = c
+        for lines_ in loops.values():
+            c = _counts(lines_)
+            if main_loop is None or c["mfma"] > main_loop["mfma"]:
+                main_loop = c
         kernels[name] = {**info, "all": _counts(body), "main_loop": main_loop}
         i = j + 1
     names = _demangle(list(kernels))

@@ -8,6 +8,7 @@ materialised attention and its autograd on the same seeded inputs.
   and not, N(0,1) inputs; output and dq/dk/dv.
 - Long context: B=1, H=16, N=16,384, D=64, inputs scaled by 0.5, causal and not; output and
   gradients, and the extra memory of forward + backward beyond inputs, outputs and gradients.
+- Strided inputs whose per-head slices span more than 2 GiB (the forward's 64-bit path).
 
 Tolerances: fp16 |err| <= 2e-3 + 2e-3 |ref| (output and gradients), fp32 1e-5 + 1e-5 |ref|.
 The float32 reference is computed a few heads at a time so its N x N matrices stay near 1 GiB."""
@@ -112,3 +113,22 @@ def test_long_context_scaled_inputs_and_memory(causal):
     extra = torch.cuda.max_memory_allocated(DEV) - base - 4 * q.numel() * q.element_size()
     # M and delta: 2 x [1, 16, 16384] float32 = 2 MiB.
     assert extra <= 2 * 16 * 16384 * 4 + (1 << 20), f"extra memory {extra / 2**20:.1f} MiB"
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_forward_slices_beyond_2gib(causal):
+    """q, k, v rows 2.125 MiB apart (views into one buffer): each head's slice spans more than
+    2 GiB, so the forward takes its 64-bit addressing path; values as for compact inputs."""
+    from tattn import attention
+
+    n, d, row = 1024, 64, (1 << 20) + (1 << 16)  # row stride in elements
+    buf = torch.empty((n - 1) * row + 3 * d, device=DEV, dtype=torch.float16)
+    views = [buf.as_strided((1, 1, n, d), (0, 0, row, 1), storage_offset=i * d) for i in range(3)]
+    for i, t in enumerate(views):
+        t.copy_(rand((1, 1, n, d), torch.float16, 50 + i, DEV))
+    q, k, v = views
+    assert (n - 1) * row * 2 > 1 << 31
+    got = attention(q, k, v, causal=causal)
+    want = naive_attention(q.float(), k.float(), v.float(), causal=causal)
+    torch.testing.assert_close(got.float(), want, **F16_TOL)
+    del buf

@@ -103,15 +103,21 @@ const TileEntry* config_entry(int kernel, int64_t D, int dtype, int id) {
 // below are the fastest entries measured on an MI355X at 16,384 tokens per batch, H=16. Entry 0
 // of each table is its general-purpose tile.
 int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N) {
-  if (dtype == TATTN_F32 || D != 64) return 0;  // fp16 and bf16 share the picks
+  if (dtype == TATTN_F32) return 0;  // fp16 and bf16 share the picks
   switch (kernel) {
     case TATTN_K_FWD:  // short rows: 128-row blocks; long: 256 rows (causal) or 512 rows
+      if (D == 128) return 0;
       if (causal) return N >= 8192 ? 0 : 1;
-      return N >= 8192 ? 3 : N >= 1024 ? 0 : 1;
+      if (D == 64) return N >= 8192 ? 3 : N >= 1024 ? 0 : 1;
+      return D == 16 && N < 2048 ? 1 : 0;
     case TATTN_K_BWD_DKDV:  // pipelined, 4 waves (128 keys) or 8 waves (256 keys)
+      if (D == 128) return 2;  // pipelined at one wave per SIMD (K, V and dK/dV in 512 registers)
+      if (D != 64) return 0;
       if (!causal) return 1;
       return N >= 2048 ? 1 : 0;
     case TATTN_K_BWD_DQ:
+      if (D == 128) return 2;
+      if (D != 64) return 0;
       return N >= 2048 ? 1 : 0;
   }
   return 0;

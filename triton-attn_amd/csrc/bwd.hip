@@ -623,7 +623,7 @@ static int launch_dkdv_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(e.nw * 64);
   if constexpr (e.pipe == 1) {
-    static_assert(sizeof(T) == 2 && D <= 64 && e.tiles == 1 && e.other == 32, "pipelined dK/dV shape");
+    static_assert(sizeof(T) == 2 && D <= 128 && e.tiles == 1 && e.other == 32, "pipelined dK/dV shape");
     if (slice_fits32(p, D)) {
       if (causal)
         dkdv_pipe_kernel<T, D, e.nw, e.occ, true><<<grid, block, 0, st>>>(p);
@@ -656,7 +656,7 @@ static int launch_dq_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(e.nw * 64);
   if constexpr (e.pipe == 1) {
-    static_assert(sizeof(T) == 2 && D <= 64 && e.tiles == 1 && e.other == 32, "pipelined dQ shape");
+    static_assert(sizeof(T) == 2 && D <= 128 && e.tiles == 1 && e.other == 32, "pipelined dQ shape");
     if (slice_fits32(p, D)) {
       if (causal)
         dq_pipe_kernel<T, D, e.nw, e.occ, true><<<grid, block, 0, st>>>(p);

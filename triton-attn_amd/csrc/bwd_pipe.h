@@ -1,4 +1,5 @@
-// Software-pipelined 16-bit (fp16, bf16) backward kernels for gfx950 (head dims 16, 32, 64).
+// Software-pipelined 16-bit (fp16, bf16) backward kernels for gfx950 (head dims 16, 32, 64 and
+// 128; at 128 the table runs them at one wave per SIMD, with the 512-register budget).
 //
 // Same math and rounding points as the generic kernels in bwd.hip (the reference's
 // src/tattn/kernels.py:151-321); the difference is the schedule. Each 32-row step issues

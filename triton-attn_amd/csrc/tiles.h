@@ -56,7 +56,7 @@ template <typename T, int D> struct DkdvTable;
 TATTN_TABLE16(DkdvTable, 16, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {4, 2, 32, 2, 0})
 TATTN_TABLE16(DkdvTable, 32, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {4, 2, 32, 2, 0})
 TATTN_TABLE16(DkdvTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {8, 1, 64, 2, 0}, {4, 2, 32, 2, 0})
-TATTN_TABLE16(DkdvTable, 128, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
+TATTN_TABLE16(DkdvTable, 128, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 1, 1})
 TATTN_TABLE(DkdvTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DkdvTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DkdvTable, float, 64, {4, 1, 32, 2, 0})
@@ -67,7 +67,7 @@ template <typename T, int D> struct DqTable;
 TATTN_TABLE16(DqTable, 16, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0})
 TATTN_TABLE16(DqTable, 32, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0})
 TATTN_TABLE16(DqTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {8, 1, 64, 2, 0})
-TATTN_TABLE16(DqTable, 128, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
+TATTN_TABLE16(DqTable, 128, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 1, 1})
 TATTN_TABLE(DqTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DqTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DqTable, float, 64, {4, 1, 32, 2, 0})

@@ -306,10 +306,11 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_generic_kernel(const FwdParams
 // 32 keys per step. Each step issues 16 MFMAs that do not depend on the step's softmax:
 // S_{i+1} = K_{i+1} Q^T and O^T += V_{i-1}^T P_{i-1}^T (the previous step's probabilities,
 // kept in registers), so the matrix cores stay busy while the VALU runs the softmax of step i.
-// Unmasked steps skip the row max: probabilities use the running max as it stands and a
-// per-lane sum check sends the wave to a slow path (row max, rescale, S recomputed from the
-// K tile still in LDS) only when some probability could exceed 2^12, which after the first
-// step is rare. Masked steps (diagonal, sequence end) always take the full softmax.
+// Steps skip the row max: probabilities use the running max as it stands (seeded with step 0's
+// row max) and a per-lane sum check sends the wave to a slow path (row max, rescale, S
+// recomputed from the K tile still in LDS) only when some probability could exceed 2^12,
+// which is rare. Masked steps (diagonal, sequence end) take the same path with keys hidden per
+// 32x32 tile.
 // LDS rings of four tiles each, filled by LDS DMA (range-checked buffer loads that write LDS
 // directly, no registers): step i reads K_{i+1} (and K_i on the slow path) and V_{i-1}, and
 // starts K_{i+3} and V_{i+1}, which have two steps to arrive; one barrier per step. Rows past
@@ -658,8 +659,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   // Steps before n_full need no mask for any wave of the workgroup (all keys below the
   // workgroup's first query row and inside the sequence): they run four per trip so ring
   // slots are constants and the S / P registers swap roles without copies. Tiles fetched past
-  // the sequence end are harmless (zeros into a free slot). Later steps mask per element and
-  // let waves above their diagonal idle.
+  // the sequence end are harmless (zeros into a free slot). Later steps mask per tile and let
+  // waves above their diagonal idle.
   const int n_full = CAUSAL ? min((qblk + 1) / 32, N / 32) : N / 32;
 
   // Full step i with i % 4 == IV: PV of step i-1 (pprev), S of step i+1, softmax of step i;

@@ -253,3 +253,82 @@ def test_inference_path_matches_autograd_path(causal, dtype):
     o2, m2 = _forward(q, k, v, causal, 0.125, save_lse=False)
     o3, m3 = _forward(q, k, v, causal, 0.125)
     assert m2 is None and m3 is not None and torch.equal(o2, o3)
+
+
+def _stress_inputs(kind, dtype, n, d=64):
+    g = torch.Generator().manual_seed(123 + n)
+    q, k, v, do = (torch.randn(1, 2, n, d, generator=g) for _ in range(4))
+    if kind == "peaked":  # scores ~ +-100: near one-hot rows
+        q, k = 10 * q, 10 * k
+    elif kind in ("rising", "falling"):
+        # Every query points along one direction; key j's projection on it grows (falls) with j,
+        # so each 32-key block raises (never raises) the running max of every row: the slow path
+        # (row max, accumulator rescale) runs on every step (never runs after step 0).
+        u = torch.randn(d, generator=g)
+        u = u / u.norm()
+        ramp = torch.linspace(-6.0, 6.0, n) if kind == "rising" else torch.linspace(6.0, -6.0, n)
+        q = 4.0 * u.expand(1, 2, n, d).clone()
+        k = k * 0.1 + ramp[None, None, :, None] * u * 2.0
+    elif kind == "mixed":  # rows of very different magnitude in one tile
+        scale = torch.logspace(-2, 1.3, n)[None, None, :, None]
+        q = q * scale
+    return (t.to(DEV, dtype) for t in (q, k, v, do))
+
+
+def _emulated_backward(q, k, v, o, m, do, causal, scale):
+    """The backward with the reference kernels' rounding points (kernels.py:151-337), in
+    float32 on materialised matrices: delta from the stored (rounded) O, P = exp2(S c - M) from
+    the saved M, P and dS rounded to the input dtype before the products that use them.
+    Returns (dq, dk, dv) and, per element, the change that one-ulp flips of those rounded
+    operands can cause (2u sum |dS||K| scale, 2u sum |dS||Q| scale, 2u sum |P||dO|): a last-bit
+    difference upstream (summation order of S) may move a value across a rounding boundary."""
+    dt = q.dtype
+    qf, kf, vf, dof = (t.float() for t in (q, k, v, do))
+    c = scale * LOG2E
+    s = qf @ kf.transpose(-1, -2).contiguous() * c
+    if causal:
+        n = q.shape[-2]
+        s = s.masked_fill(torch.ones(n, n, device=q.device, dtype=torch.bool).triu(1), float("-inf"))
+    p = torch.exp2(s - m[..., None])
+    delta = (dof * o.float()).sum(-1)
+    dv = p.to(dt).float().transpose(-1, -2).contiguous() @ dof
+    dp = dof @ vf.transpose(-1, -2).contiguous()
+    ds = (p * (dp - delta[..., None])).to(dt).float()
+    dq = ds @ kf * scale
+    dk = ds.transpose(-1, -2).contiguous() @ qf * scale
+    two_u = 2.0 ** -10 if dt == torch.float16 else 2.0 ** -7
+    bq = two_u * scale * (ds.abs() @ kf.abs())
+    bk = two_u * scale * (ds.abs().transpose(-1, -2).contiguous() @ qf.abs())
+    bv = two_u * (p.transpose(-1, -2).contiguous() @ dof.abs())
+    return (dq, dk, dv), (bq, bk, bv)
+
+
+@pytest.mark.parametrize("kind", ["peaked", "rising", "falling", "mixed"])
+@pytest.mark.parametrize("n", [200, 1024])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_softmax_stress_matches_definition(kind, n, causal, dtype):
+    """Inputs that drive the max-free softmax through its slow path (rising scores: a new row
+    max in every key block) or keep it off it, plus near one-hot and mixed-magnitude rows.
+    Output against float32 attention; M against the float32 log-sum-exp; gradients against the
+    backward with the reference kernels' rounding points (near one-hot rows make dP - delta
+    cancel, so the rounding of the stored O dominates their gradients in any fp16 FlashAttention
+    and float32 autograd is not the right yardstick there)."""
+    from tattn.api import _backward, _forward
+
+    q, k, v, do = _stress_inputs(kind, dtype, n)
+    scale = 0.125
+    o, m = _forward(q, k, v, causal, scale)
+    ref = naive_attention(q.float(), k.float(), v.float(), causal=causal, sm_scale=scale)
+    t = tol(dtype)
+    assert torch.isfinite(o).all() and torch.isfinite(m).all()
+    torch.testing.assert_close(o.float(), ref, **t)
+    sf = q.float() @ k.float().transpose(-1, -2).contiguous() * scale
+    if causal:
+        sf = sf.masked_fill(torch.ones(n, n, device=DEV, dtype=torch.bool).triu(1), float("-inf"))
+    torch.testing.assert_close(m, torch.logsumexp(sf, -1) * LOG2E, atol=8e-3, rtol=1e-4)
+    got = _backward(q, k, v, o, m, do, causal, scale)
+    want, flips = _emulated_backward(q, k, v, o, m, do, causal, scale)
+    for name, g_, w, bnd in zip(("dq", "dk", "dv"), got, want, flips):
+        excess = ((g_.float() - w).abs() - t["atol"] - t["rtol"] * w.abs() - bnd).max().item()
+        assert excess <= 0, f"{name}: error exceeds the bound by {excess:.3e}"

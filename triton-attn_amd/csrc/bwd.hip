@@ -152,8 +152,9 @@ struct DkdvCfg {
   static constexpr int LDS = 2 * STAGE;
 };
 
-template <typename T, int D, int NW, int KTW, int BMQ, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64, 2) void dkdv_kernel(const BwdParams p) {
+// OCC: waves per SIMD the register budget is sized for (1 gives 512 registers: D=128).
+template <typename T, int D, int NW, int KTW, int BMQ, bool CAUSAL, int OCC>
+__global__ __launch_bounds__(NW * 64, OCC) void dkdv_kernel(const BwdParams p) {
   using C = DkdvCfg<T, D, NW, KTW, BMQ>;
   using E = Elt<T>;
   using Op = typename E::Op;
@@ -379,8 +380,9 @@ struct DqCfg {
   static constexpr int LDS = 2 * STAGE;
 };
 
-template <typename T, int D, int NW, int QTW, int BNK, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64, 2) void dq_kernel(const BwdParams p) {
+// OCC: waves per SIMD the register budget is sized for (1 gives 512 registers: D=128).
+template <typename T, int D, int NW, int QTW, int BNK, bool CAUSAL, int OCC>
+__global__ __launch_bounds__(NW * 64, OCC) void dq_kernel(const BwdParams p) {
   using C = DqCfg<T, D, NW, QTW, BNK>;
   using E = Elt<T>;
   using Op = typename E::Op;
@@ -634,14 +636,14 @@ static int launch_dkdv_entry(const BwdParams& p0, bool causal, hipStream_t st) {
     p.n_blocks = (p.N + 127) / 128;  // slices beyond 2 GiB: 64-bit addressing
     const dim3 g2((unsigned)((int64_t)p.n_blocks * p.Z * p.H));
     if (causal)
-      dkdv_kernel<T, D, 4, 1, 64, true><<<g2, dim3(256), 0, st>>>(p);
+      dkdv_kernel<T, D, 4, 1, 32, true, D == 128 ? 1 : 2><<<g2, dim3(256), 0, st>>>(p);
     else
-      dkdv_kernel<T, D, 4, 1, 64, false><<<g2, dim3(256), 0, st>>>(p);
+      dkdv_kernel<T, D, 4, 1, 32, false, D == 128 ? 1 : 2><<<g2, dim3(256), 0, st>>>(p);
   } else {
     if (causal)
-      dkdv_kernel<T, D, e.nw, e.tiles, e.other, true><<<grid, block, 0, st>>>(p);
+      dkdv_kernel<T, D, e.nw, e.tiles, e.other, true, e.occ><<<grid, block, 0, st>>>(p);
     else
-      dkdv_kernel<T, D, e.nw, e.tiles, e.other, false><<<grid, block, 0, st>>>(p);
+      dkdv_kernel<T, D, e.nw, e.tiles, e.other, false, e.occ><<<grid, block, 0, st>>>(p);
   }
   return check_launch("tattn_bwd_dkdv");
 }
@@ -667,14 +669,14 @@ static int launch_dq_entry(const BwdParams& p0, bool causal, hipStream_t st) {
     p.n_blocks = (p.N + 127) / 128;  // slices beyond 2 GiB: 64-bit addressing
     const dim3 g2((unsigned)((int64_t)p.n_blocks * p.Z * p.H));
     if (causal)
-      dq_kernel<T, D, 4, 1, 32, true><<<g2, dim3(256), 0, st>>>(p);
+      dq_kernel<T, D, 4, 1, 32, true, D == 128 ? 1 : 2><<<g2, dim3(256), 0, st>>>(p);
     else
-      dq_kernel<T, D, 4, 1, 32, false><<<g2, dim3(256), 0, st>>>(p);
+      dq_kernel<T, D, 4, 1, 32, false, D == 128 ? 1 : 2><<<g2, dim3(256), 0, st>>>(p);
   } else {
     if (causal)
-      dq_kernel<T, D, e.nw, e.tiles, e.other, true><<<grid, block, 0, st>>>(p);
+      dq_kernel<T, D, e.nw, e.tiles, e.other, true, e.occ><<<grid, block, 0, st>>>(p);
     else
-      dq_kernel<T, D, e.nw, e.tiles, e.other, false><<<grid, block, 0, st>>>(p);
+      dq_kernel<T, D, e.nw, e.tiles, e.other, false, e.occ><<<grid, block, 0, st>>>(p);
   }
   return check_launch("tattn_bwd_dq");
 }

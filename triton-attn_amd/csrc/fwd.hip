@@ -53,8 +53,9 @@ struct FwdCfg {
   static_assert(D % SK == 0 && BN % 32 == 0, "tile shape");
 };
 
-template <typename T, int D, int NW, int QT, int BN, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64, 2) void fwd_generic_kernel(const FwdParams p) {
+// OCC: waves per SIMD the register budget is sized for (1 gives 512 registers: D=128 in fp32).
+template <typename T, int D, int NW, int QT, int BN, bool CAUSAL, int OCC>
+__global__ __launch_bounds__(NW * 64, OCC) void fwd_generic_kernel(const FwdParams p) {
   using C = FwdCfg<T, D, NW, QT, BN>;
   using E = Elt<T>;
   using Op = typename E::Op;
@@ -749,10 +750,10 @@ static int launch_fwd_entry(const FwdParams& p0, bool causal, hipStream_t st) {
     static_assert(e.other == 32, "the 16-bit forward runs 32 keys per step");
     if (!fits32) {  // slices beyond 2 GiB: 64-bit addressing
       if (causal)
-        fwd_generic_kernel<T, D, 4, 1, 64, true><<<dim3((unsigned)(((p.N + 127) / 128) * (int64_t)p.Z * p.H)), dim3(256), 0, st>>>(
+        fwd_generic_kernel<T, D, 4, 1, 64, true, D == 128 ? 1 : 2><<<dim3((unsigned)(((p.N + 127) / 128) * (int64_t)p.Z * p.H)), dim3(256), 0, st>>>(
             [&] { FwdParams q = p; q.n_qblocks = (p.N + 127) / 128; return q; }());
       else
-        fwd_generic_kernel<T, D, 4, 1, 64, false><<<dim3((unsigned)(((p.N + 127) / 128) * (int64_t)p.Z * p.H)), dim3(256), 0, st>>>(
+        fwd_generic_kernel<T, D, 4, 1, 64, false, D == 128 ? 1 : 2><<<dim3((unsigned)(((p.N + 127) / 128) * (int64_t)p.Z * p.H)), dim3(256), 0, st>>>(
             [&] { FwdParams q = p; q.n_qblocks = (p.N + 127) / 128; return q; }());
       return check_launch("tattn_fwd");
     }
@@ -762,9 +763,9 @@ static int launch_fwd_entry(const FwdParams& p0, bool causal, hipStream_t st) {
       fwd_pipe_kernel<T, D, e.nw, e.tiles, e.occ, false><<<grid, block, 0, st>>>(p);
   } else {
     if (causal)
-      fwd_generic_kernel<T, D, e.nw, e.tiles, e.other, true><<<grid, block, 0, st>>>(p);
+      fwd_generic_kernel<T, D, e.nw, e.tiles, e.other, true, e.occ><<<grid, block, 0, st>>>(p);
     else
-      fwd_generic_kernel<T, D, e.nw, e.tiles, e.other, false><<<grid, block, 0, st>>>(p);
+      fwd_generic_kernel<T, D, e.nw, e.tiles, e.other, false, e.occ><<<grid, block, 0, st>>>(p);
   }
   return check_launch("tattn_fwd");
 }

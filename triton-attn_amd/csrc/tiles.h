@@ -35,9 +35,10 @@ template <typename T, int D> struct FwdTable;
   TATTN_TABLE(NAME, __bf16, D, __VA_ARGS__)
 
 // Entry 0 of each table is the default pick. 16-bit forward entries and the 16-bit backward
-// entries marked pipe run the software-pipelined kernels (32 rows per step). Every entry fits
-// its register budget without scratch in the main loop and can reach its waves per SIMD
-// within the 160 KB of LDS (a D=64 forward workgroup holds 44 KB of K/V ring).
+// entries marked pipe run the software-pipelined kernels (32 rows per step). Every 16-bit
+// entry fits its register budget without scratch and can reach its waves per SIMD within the
+// 160 KB of LDS (a D=64 forward workgroup holds 44 KB of K/V ring); D=128 entries run at one
+// wave per SIMD (512 registers). Of the fp32 kernels only causal dK/dV at D=128 spills (32 bytes).
 TATTN_TABLE16(FwdTable, 16, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1})
 TATTN_TABLE16(FwdTable, 32, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1})
 TATTN_TABLE16(FwdTable, 64, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {8, 2, 32, 2, 1})
@@ -45,7 +46,7 @@ TATTN_TABLE16(FwdTable, 128, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1})
 TATTN_TABLE(FwdTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(FwdTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(FwdTable, float, 64, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
-TATTN_TABLE(FwdTable, float, 128, {4, 1, 32, 2, 0})
+TATTN_TABLE(FwdTable, float, 128, {4, 1, 32, 1, 0})
 
 }  // namespace tattn
 
@@ -55,22 +56,22 @@ namespace tattn {
 template <typename T, int D> struct DkdvTable;
 TATTN_TABLE16(DkdvTable, 16, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {4, 2, 32, 2, 0})
 TATTN_TABLE16(DkdvTable, 32, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {4, 2, 32, 2, 0})
-TATTN_TABLE16(DkdvTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {8, 1, 64, 2, 0}, {4, 2, 32, 2, 0})
-TATTN_TABLE16(DkdvTable, 128, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 1, 1})
+TATTN_TABLE16(DkdvTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 32, 2, 0})
+TATTN_TABLE16(DkdvTable, 128, {4, 1, 32, 1, 1}, {4, 1, 32, 1, 0})
 TATTN_TABLE(DkdvTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DkdvTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DkdvTable, float, 64, {4, 1, 32, 2, 0})
-TATTN_TABLE(DkdvTable, float, 128, {4, 1, 32, 2, 0})
+TATTN_TABLE(DkdvTable, float, 128, {4, 1, 32, 1, 0})
 
 // ---- backward dQ: {waves, query tiles per wave, keys per step} ------------------------------
 template <typename T, int D> struct DqTable;
 TATTN_TABLE16(DqTable, 16, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0})
 TATTN_TABLE16(DqTable, 32, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0})
-TATTN_TABLE16(DqTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {8, 1, 64, 2, 0})
-TATTN_TABLE16(DqTable, 128, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 1, 1})
+TATTN_TABLE16(DqTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {8, 1, 64, 2, 0})
+TATTN_TABLE16(DqTable, 128, {4, 1, 32, 1, 1}, {4, 1, 32, 1, 0})
 TATTN_TABLE(DqTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DqTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DqTable, float, 64, {4, 1, 32, 2, 0})
-TATTN_TABLE(DqTable, float, 128, {4, 1, 32, 2, 0})
+TATTN_TABLE(DqTable, float, 128, {4, 1, 32, 1, 0})
 
 }  // namespace tattn

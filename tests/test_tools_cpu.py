@@ -139,3 +139,22 @@ def test_report_renders_every_section():
     assert "| SDPA flash | 2.25–2.25× | 2.25–2.25× |" in text
     assert "OOM" in text and "| 16,384 (1) |" in text
     assert "16384: 3/1/1" in text
+
+
+@pytest.fixture(scope="module")
+def bwd_asm():
+    return diagnose.compile_asm(diagnose.CSRC / "bwd.hip")
+
+
+@pytest.mark.skipif(not _have_hipcc(), reason="hipcc not installed")
+def test_no_kernel_spills_registers(fwd_asm, bwd_asm):
+    """Every kernel instantiation the tile tables reach compiles without scratch (register
+    spills), except fp32 causal dK/dV at D=128 (a few bytes, not a performance path)."""
+    allowed = {"dkdv_kernel<float, 128, 4, 1, 32, true, 1>"}
+    spills = []
+    for asm in (fwd_asm, bwd_asm):
+        for k in diagnose.isa_stats(asm, "_kernelI").values():
+            name = k["name"].replace("tattn::", "").split("(")[0].removeprefix("void ")
+            if k.get("scratch_bytes_per_lane") and name not in allowed:
+                spills.append((name, k["scratch_bytes_per_lane"]))
+    assert not spills, spills

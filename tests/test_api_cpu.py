@@ -69,3 +69,23 @@ def test_config_resolution():
     assert _resolve(_lib.K_FWD, 64, torch.float16, sel, False, 128) == 0
     with pytest.raises(ValueError, match="matches 0"):
         _resolve(_lib.K_FWD, 64, torch.float16, {"BLOCK_M": 7}, False, 128)
+
+
+def test_autotune_off_by_default_and_cache_format(monkeypatch):
+    """First-use timing is opt-in (TATTN_AUTOTUNE=1 or set_autotune); while off the library's own
+    pick (-1) is used and nothing is launched; the cache reports picks per kernel and key."""
+    import tattn
+    from tattn import api
+
+    monkeypatch.setattr(api, "_tuned", {})
+    launched = []
+    monkeypatch.setattr(api, "_autotune", False)
+    assert api._tuned_id(_lib.K_FWD, torch.zeros(1), 64, False, 1000, launched.append) == -1
+    assert launched == [] and api._tuned == {}
+    tattn.set_autotune(True)
+    assert api._autotune
+    tattn.set_autotune(False)
+    assert not api._autotune
+    api._tuned[(_lib.K_BWD_DQ, 0, api._bucket(1000), 64, _lib.F16, True)] = 2
+    assert tattn.autotune_cache() == {"fwd": {}, "bwd_dkdv": {},
+                                      "bwd_dq": {"device=0, n_bucket=1024, d=64, dtype=float16, causal=True": 2}}

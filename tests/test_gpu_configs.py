@@ -49,3 +49,39 @@ def test_config_forward_and_backward(kernel, dtype, d, cid):
             for name, got, want in zip(("dq", "dk", "dv"), (dq, dk, dv), (qr.grad, kr.grad, vr.grad)):
                 torch.testing.assert_close(got.float(), want, atol=tol, rtol=tol,
                                            msg=lambda s: f"{name} n={n} causal={causal}: {s}")
+
+
+def test_autotune_first_use_times_once_and_stays_correct(monkeypatch):
+    """With first-use timing on, the first fwd+bwd of a key times every table entry, keeps a valid
+    entry per kernel and matches the definition; a second call of the same key (another length
+    in the same power-of-two bucket) reuses the picks without timing again."""
+    import tattn
+    from tattn import _lib, api
+
+    monkeypatch.setattr(api, "_tuned", {})
+    tattn.set_autotune(True)
+    timed = []
+    real = _lib.num_configs
+    monkeypatch.setattr(_lib, "num_configs", lambda *a: timed.append(a) or real(*a))
+    try:
+        for n in (600, 1000):
+            for causal in (False, True):
+                q, k, v, do = (rand((2, 4, n, 64), torch.float16, 11 * n + s, DEV) for s in range(4))
+                qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+                o = tattn.attention(qg, kg, vg, causal=causal)
+                o.backward(do)
+                qr, kr, vr = (t.float().requires_grad_() for t in (q, k, v))
+                ref = naive_attention(qr, kr, vr, causal=causal)
+                ref.backward(do.float())
+                for name, got, want in zip(("o", "dq", "dk", "dv"), (o, qg.grad, kg.grad, vg.grad),
+                                           (ref, qr.grad, kr.grad, vr.grad)):
+                    torch.testing.assert_close(got.float(), want.detach(), atol=2e-3, rtol=2e-3,
+                                               msg=lambda s: f"{name} n={n} causal={causal}: {s}")
+    finally:
+        tattn.set_autotune(False)
+    assert len(timed) == 6  # three kernels x two masks, all at n=600; n=1000 shares the bucket
+    cache = tattn.autotune_cache()
+    for kernel, kid in (("fwd", _lib.K_FWD), ("bwd_dkdv", _lib.K_BWD_DKDV), ("bwd_dq", _lib.K_BWD_DQ)):
+        assert len(cache[kernel]) == 2
+        for cid in cache[kernel].values():
+            assert 0 <= cid < real(kid, 64, _lib.F16)

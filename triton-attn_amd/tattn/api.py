@@ -12,7 +12,8 @@ raises instead of computing.
 from __future__ import annotations
 
 import math
-from typing import Any, Union
+import os
+from typing import Any, Callable, Union
 
 import torch
 from torch.autograd.function import once_differentiable
@@ -112,6 +113,60 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+# Optional first-use timing of the tile table. The reference autotunes on the first call of each
+# (N bucket, head dim, causal) key (src/tattn/kernels.py:57-61, 151-155, 242-246); here the
+# measured picks of the library are the default and timing is opt-in: TATTN_AUTOTUNE=1 in the
+# environment, or set_autotune(True). The first call of a key then times every table entry on
+# the caller's stream (HIP events; skipped while a graph is being captured) and keeps the
+# fastest for that key.
+_autotune = os.environ.get("TATTN_AUTOTUNE", "0") not in ("", "0")
+_tuned: dict[tuple[int, int, int, int, bool, int], int] = {}
+
+
+def set_autotune(on: bool) -> None:
+    """Turn first-use timing of the tile table on or off (the cache is kept)."""
+    global _autotune
+    _autotune = bool(on)
+
+
+def autotune_cache() -> dict[str, dict[str, int]]:
+    """Entries chosen by timing so far: {kernel: {"device=.., n_bucket=.., d=.., dtype=..,
+    causal=..": table id}} (the analog of the reference bench's dump of its autotune caches)."""
+    out: dict[str, dict[str, int]] = {name: {} for name in _lib.KERNEL_NAMES.values()}
+    for (kernel, dev, bucket, d, code, causal), cid in _tuned.items():
+        dtype = str({c: t for t, c in _DTYPES.items()}[code]).removeprefix("torch.")
+        key = f"device={dev}, n_bucket={bucket}, d={d}, dtype={dtype}, causal={causal}"
+        out[_lib.KERNEL_NAMES[kernel]][key] = cid
+    return out
+
+
+def _tuned_id(kernel: int, t: torch.Tensor, d: int, causal: bool, n: int,
+              launch: Callable[[int], int]) -> int:
+    """The table entry for this call: -1 (the library's pick) unless autotuning is on; then the
+    fastest entry for the key, timed on first use by running `launch(id)` for every entry."""
+    if not _autotune or torch.cuda.is_current_stream_capturing():
+        return -1
+    code = _DTYPES[t.dtype]
+    key = (kernel, t.device.index or 0, _bucket(n), d, code, causal)
+    if key not in _tuned:
+        stream = torch.cuda.current_stream(t.device)
+        best, best_ms = -1, float("inf")
+        for cid in range(_lib.num_configs(kernel, d, code)):
+            if launch(cid) != 0:  # not usable for this call: skip
+                continue
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(3):
+                launch(cid)
+            end.record(stream)
+            end.synchronize()
+            ms = start.elapsed_time(end)
+            if ms < best_ms:
+                best, best_ms = cid, ms
+        _tuned[key] = best
+    return _tuned[key]
+
+
 def _forward(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: float,
     config: Config = None, *, save_lse: bool = True,
@@ -125,12 +180,13 @@ def _forward(
     o = torch.empty_like(q)
     m = torch.empty((z, h, n), device=q.device, dtype=torch.float32) if save_lse else None
     cid = _resolve(_lib.K_FWD, d, q.dtype, config, causal, n)
-    with torch.cuda.device(q.device):
-        rc = lib.tattn_fwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), m.data_ptr() if m is not None else None,
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), m.data_ptr() if m is not None else None,
             _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(o),
-            z, h, n, d, _DTYPES[q.dtype], int(causal), float(scale), cid, _stream(q),
-        )
+            z, h, n, d, _DTYPES[q.dtype], int(causal), float(scale))
+    with torch.cuda.device(q.device):
+        if config is None:
+            cid = _tuned_id(_lib.K_FWD, q, d, causal, n, lambda c: lib.tattn_fwd(*args, c, _stream(q)))
+        rc = lib.tattn_fwd(*args, cid, _stream(q))
     _lib.check(rc, "tattn_fwd")
     return o, m
 
@@ -157,16 +213,18 @@ def _backward(
     st = _lib.strides4(q)
     code = _DTYPES[q.dtype]
     stream = _stream(q)
+    dkdv_args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                 m.data_ptr(), delta.data_ptr(), st, z, h, n, d, code, int(causal), float(scale))
+    dq_args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), dq.data_ptr(), m.data_ptr(),
+               delta.data_ptr(), st, z, h, n, d, code, int(causal), float(scale))
     with torch.cuda.device(q.device):
         _lib.check(lib.tattn_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta.data_ptr(), st,
                                             z, h, n, d, code, stream), "tattn_bwd_preprocess")
-        _lib.check(lib.tattn_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                                      dk.data_ptr(), dv.data_ptr(), m.data_ptr(), delta.data_ptr(),
-                                      st, z, h, n, d, code, int(causal), float(scale), kid, stream),
-                   "tattn_bwd_dkdv")
-        _lib.check(lib.tattn_bwd_dq(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                                    dq.data_ptr(), m.data_ptr(), delta.data_ptr(), st, z, h, n, d,
-                                    code, int(causal), float(scale), qid, stream), "tattn_bwd_dq")
+        if config is None:
+            kid = _tuned_id(_lib.K_BWD_DKDV, q, d, causal, n, lambda c: lib.tattn_bwd_dkdv(*dkdv_args, c, stream))
+            qid = _tuned_id(_lib.K_BWD_DQ, q, d, causal, n, lambda c: lib.tattn_bwd_dq(*dq_args, c, stream))
+        _lib.check(lib.tattn_bwd_dkdv(*dkdv_args, kid, stream), "tattn_bwd_dkdv")
+        _lib.check(lib.tattn_bwd_dq(*dq_args, qid, stream), "tattn_bwd_dq")
     return dq, dk, dv
 
 

@@ -4,7 +4,9 @@ The counterpart of the reference's benchmark (bench/bench.py:1-206): for every s
 (batch x seq held at a fixed token count), causal and not, forward and forward+backward, it
 times
 
-  - tattn (this package's HIP kernels, table-picked tiles),
+  - tattn (this package's HIP kernels, table-picked tiles, or with --autotune the fastest
+    table entry timed on first use; the picks are recorded as the reference records its
+    autotune caches, bench/bench.py:176-201),
   - torch SDPA with each backend (flash, memory-efficient, math), one at a time,
   - naive materialised attention (the definition),
 
@@ -16,7 +18,7 @@ autograd at N = 1024 and 4096, and a plain fp16 4096^3 matmul as a GEMM-rate ref
 implementation cannot run (unsupported backend, out of memory) are recorded, not fatal.
 
     python -m tattn.benchsuite [--seqs 512,...,16384] [--tokens 16384] [--heads 16] [--dim 64]
-                               [--out results/<gpu>.json]
+                               [--autotune] [--out results/<gpu>.json]
 
 Render the result with `python -m tattn.report results/<gpu>.json`.
 """
@@ -33,7 +35,7 @@ from typing import Any, Callable
 import torch
 import torch.nn.functional as F
 
-from . import attention
+from . import attention, autotune_cache, set_autotune
 from . import _lib
 from .timing import do_bench
 
@@ -104,7 +106,7 @@ def measure(fn: Callable[[], Any], clear: Callable[[], None] = lambda: None) -> 
         return {"error": str(e).splitlines()[0][:200]}
 
 
-def run(seqs: list[int], tokens: int, heads: int, dim: int) -> dict[str, Any]:
+def run(seqs: list[int], tokens: int, heads: int, dim: int, autotune: bool = False) -> dict[str, Any]:
     dev = torch.device("cuda")
     _lib.load()
     props = torch.cuda.get_device_properties(dev)
@@ -112,6 +114,7 @@ def run(seqs: list[int], tokens: int, heads: int, dim: int) -> dict[str, Any]:
     rows: list[dict[str, Any]] = []
     accuracy: list[dict[str, Any]] = []
     picks: dict[str, dict[str, int]] = {}
+    set_autotune(autotune)
     for n in seqs:
         b = max(1, tokens // n)
         for causal in (False, True):
@@ -190,6 +193,7 @@ def run(seqs: list[int], tokens: int, heads: int, dim: int) -> dict[str, Any]:
         "rows": rows,
         "accuracy": accuracy,
         "table_picks": picks,
+        "tuned_configs": autotune_cache() if autotune else None,
     }
 
 
@@ -199,11 +203,12 @@ def main() -> None:
     ap.add_argument("--tokens", type=int, default=16384, help="batch * seq held constant")
     ap.add_argument("--heads", type=int, default=16)
     ap.add_argument("--dim", type=int, default=64)
+    ap.add_argument("--autotune", action="store_true", help="time the tile table on first use")
     ap.add_argument("--out", default=None)
     a = ap.parse_args()
     if not torch.cuda.is_available():
         raise SystemExit("needs a ROCm GPU")
-    res = run([int(x) for x in a.seqs.split(",")], a.tokens, a.heads, a.dim)
+    res = run([int(x) for x in a.seqs.split(",")], a.tokens, a.heads, a.dim, a.autotune)
     name = res["env"]["arch"].split(":")[0] or res["env"]["gpu"].replace(" ", "_").lower()
     out = Path(a.out) if a.out else REPO / "results" / f"{name}.json"
     out.parent.mkdir(parents=True, exist_ok=True)

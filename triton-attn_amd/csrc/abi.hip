@@ -107,16 +107,16 @@ int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N) {
   switch (kernel) {
     case TATTN_K_FWD:  // short rows: 128-row blocks; long: 256 rows (causal) or 512 rows
       if (D == 128) return 0;
-      if (causal) return N >= 8192 ? 0 : 1;
+      if (causal) return N >= 4096 ? 0 : 1;
       if (D == 64) return N >= 4096 ? 3 : N >= 1024 ? 0 : 1;
       return D == 16 && N < 2048 ? 1 : 0;
     case TATTN_K_BWD_DKDV:  // pipelined, 4 waves (128 keys) or 8 waves (256 keys)
       if (D != 64) return 0;  // D=128: entry 0 is pipelined at one wave per SIMD (512 registers)
       if (!causal) return 1;
-      return N >= 2048 ? 1 : 0;
-    case TATTN_K_BWD_DQ:  // 8 waves from N = 2048, except long non-causal rows (4 waves, 2-3% faster)
+      return N >= 2048 ? 1 : N >= 1024 ? 0 : 2;
+    case TATTN_K_BWD_DQ:  // 4 waves, except non-causal 2048 <= N < 8192 (8 waves, up to 2% faster)
       if (D != 64) return 0;
-      return N >= 2048 && (causal || N < 8192) ? 1 : 0;
+      return !causal && N >= 2048 && N < 8192 ? 1 : 0;
   }
   return 0;
 }

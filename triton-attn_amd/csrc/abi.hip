@@ -110,7 +110,7 @@ int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N) {
       if (causal) return N >= 4096 ? 0 : 1;
       if (D == 64) return N >= 4096 ? 3 : N >= 1024 ? 0 : 1;
       return D == 16 && N < 2048 ? 1 : 0;
-    case TATTN_K_BWD_DKDV:  // pipelined, 4 waves (128 keys) or 8 waves (256 keys)
+    case TATTN_K_BWD_DKDV:  // pipelined, 4 waves (128 keys) or 8 waves (256 keys); causal N < 1024: generic
       if (D != 64) return 0;  // D=128: entry 0 is pipelined at one wave per SIMD (512 registers)
       if (!causal) return 1;
       return N >= 2048 ? 1 : N >= 1024 ? 0 : 2;

@@ -1,7 +1,7 @@
 """Test oracle for the tattn attention path.
 
 THIS PACKAGE IS TEST INFRASTRUCTURE. Only `tests/`, `__graft_entry__.smoke()` and the
-`cpu_baseline` leg of `bench.py` may import it, and only as the checker (or, for the
+`cpu_baseline` leg of `bench.py` may import it, and only to check results (or, for the
 baseline, as the thing timed on the host CPU). The product package `tattn` never imports it:
 on a GPU it runs the HIP kernels or raises.
 

@@ -35,7 +35,7 @@ def _gpu():
         pytest.skip("no GPU")
     from tattn import hip_available
 
-    # On a GPU box the HIP library must load and run: never skip silently there.
+    # With a GPU present the HIP library must load and run: never skip silently.
     assert hip_available(DEV), "libtattn_hip.so did not load or the device is not a gfx950"
 
 

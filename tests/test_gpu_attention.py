@@ -184,6 +184,22 @@ def test_single_key(dtype, causal):
     assert q.grad.abs().max() <= 1e-6 and k.grad.abs().max() <= 1e-6
 
 
+@pytest.mark.parametrize("shape", [(0, 2, 16, 64), (2, 0, 16, 64), (2, 3, 0, 32)])
+def test_empty_inputs_give_empty_outputs(shape):
+    """No rows to attend over: empty output and empty gradients of the inputs' shape, nothing
+    launched (the reference's grid is empty then)."""
+    from tattn import attention
+
+    q, k, v = (torch.zeros(shape, device=DEV, dtype=torch.float16, requires_grad=True) for _ in range(3))
+    for causal in (False, True):
+        out = attention(q, k, v, causal=causal)
+        assert out.shape == q.shape and out.dtype == q.dtype
+        out.backward(torch.zeros_like(out))
+        assert q.grad.shape == k.grad.shape == v.grad.shape == q.shape
+        with torch.no_grad():
+            assert attention(q, k, v, causal=causal).shape == q.shape
+
+
 def test_zero_queries_give_mean_and_cumulative_mean():
     from tattn import attention
 

@@ -180,6 +180,8 @@ def _forward(
     o = torch.empty_like(q)
     m = torch.empty((z, h, n), device=q.device, dtype=torch.float32) if save_lse else None
     cid = _resolve(_lib.K_FWD, d, q.dtype, config, causal, n)
+    if q.numel() == 0:  # no rows: nothing to launch (the reference's empty grid launches nothing)
+        return o, m
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), m.data_ptr() if m is not None else None,
             _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(o),
             z, h, n, d, _DTYPES[q.dtype], int(causal), float(scale))
@@ -204,6 +206,8 @@ def _backward(
     m = m.contiguous()
     delta = torch.empty((z, h, n), device=q.device, dtype=torch.float32)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    if q.numel() == 0:
+        return dq, dk, dv
     if isinstance(config, dict) and ("dkdv" in config or "dq" in config):
         kid = _resolve(_lib.K_BWD_DKDV, d, q.dtype, config.get("dkdv"), causal, n)
         qid = _resolve(_lib.K_BWD_DQ, d, q.dtype, config.get("dq"), causal, n)

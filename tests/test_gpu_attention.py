@@ -226,6 +226,43 @@ def test_run_to_run_bitwise_identical(causal):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_graph_capture_and_replay(causal):
+    """Forward + backward captured into one HIP graph (the library allocates nothing and
+    enqueues only kernels on the current stream) and replayed on new inputs, with eager work and
+    synchronisation between replays: every replay gives the eager result's bits."""
+    from tattn import attention
+
+    shape = (2, 4, 300, 64)
+    q, k, v = (r(shape, torch.float16, 400 + s).requires_grad_() for s in range(3))
+    do = r(shape, torch.float16, 403)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up off the capture stream, as torch requires
+        for _ in range(2):
+            q.grad = k.grad = v.grad = None
+            attention(q, k, v, causal=causal).backward(do)
+    torch.cuda.current_stream().wait_stream(side)
+    q.grad = k.grad = v.grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = attention(q, k, v, causal=causal)
+        out.backward(do)
+    for rep in range(3):
+        new = [r(shape, torch.float16, 500 + 10 * rep + s) for s in range(4)]
+        with torch.no_grad():
+            for dst, src in zip((q, k, v, do), new):
+                dst.copy_(src)
+        graph.replay()
+        qe, ke, ve = (t.clone().requires_grad_() for t in new[:3])
+        oe = attention(qe, ke, ve, causal=causal)  # eager work between replays
+        oe.backward(new[3])
+        torch.cuda.synchronize()
+        for name, got, want in (("o", out, oe), ("dq", q.grad, qe.grad), ("dk", k.grad, ke.grad),
+                                ("dv", v.grad, ve.grad)):
+            assert torch.equal(got, want), (rep, name)
+
+
 def test_uses_current_stream():
     """Work is enqueued on the caller's current stream (no host sync inside the call)."""
     from tattn import attention

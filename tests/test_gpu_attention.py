@@ -226,6 +226,30 @@ def test_run_to_run_bitwise_identical(causal):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("causal", [False, True])
+def test_whole_backward_entry_point_matches_three_launches(dtype, causal):
+    """`tattn_bwd` (preprocess, dK/dV and dQ in one call) gives the bits of the three separate
+    entry points, and delta is the preprocess's rowsum(dO * O)."""
+    from tattn import _lib
+    from tattn.api import _DTYPES, _backward, _forward
+
+    q, k, v, do = (r((2, 3, 333, 64), dtype, 600 + s) for s in range(4))
+    o, m = _forward(q, k, v, causal, 0.125)
+    want = _backward(q, k, v, o, m, do, causal, 0.125)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    delta = torch.empty((2, 3, 333), device=DEV, dtype=torch.float32)
+    rc = _lib.load().tattn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+                               dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), m.data_ptr(), delta.data_ptr(),
+                               _lib.strides4(q), 2, 3, 333, 64, _DTYPES[dtype], int(causal), 0.125, -1,
+                               torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "tattn_bwd")
+    torch.cuda.synchronize()
+    for name, got, ref in zip(("dq", "dk", "dv"), (dq, dk, dv), want):
+        assert torch.equal(got, ref), name
+    torch.testing.assert_close(delta, (do.float() * o.float()).sum(-1), atol=1e-5, rtol=1e-5)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_graph_capture_and_replay(causal):
     """Forward + backward captured into one HIP graph (the library allocates nothing and

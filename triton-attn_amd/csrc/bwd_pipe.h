@@ -269,10 +269,17 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
   };
 
   int i = 0;
-  // Causal: the workgroup's first NW query blocks cross its keys' diagonal; mask them.
+  // Causal: the workgroup's first NW query blocks cross its keys' diagonal; mask them. Query
+  // block i < w lies wholly before wave w's keys (P = dS = 0): the wave skips its MFMAs and
+  // softmax there and only stages tiles, leaving its SIMD to the other waves.
   const int n_mask = CAUSAL ? min(nsteps, NW) : 0;
   for (; i < n_mask; ++i) {
-    step(i, i & 3, sa, da, sb, db, pa, dsa, pb, dsb, std::true_type{});
+    gload(i + 2);
+    if (i + 1 >= w) qk(sb, db, (i + 1) & 3);
+    if (i - 1 >= w) grad_mma(pa, dsa, (i + 3) & 3);
+    if (i >= w) pds(sa, da, pb, dsb, i & 3, lo + 32 * i, std::true_type{});
+    lstore((i + 2) & 3);
+    __syncthreads();
     roll();
   }
   for (; i + 3 < nsteps; i += 4) {  // i % 4 == 0 here (NW is a multiple of 4)

@@ -1,0 +1,50 @@
+"""bench.py's output contract: one JSON line with the metric, whole-job value, roofline of the
+forward kernel and the CPU baseline; a single GPU only."""
+
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def test_more_than_one_gpu_is_refused_with_a_message():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_recorded_traffic_is_read_from_the_profile():
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    t = bench.measured_traffic()
+    algorithmic = 4 * 33554432 + 1048576  # Q, K, V read, O written (16k tokens x 16 heads x 64 fp16), M
+    assert t is not None and algorithmic <= t < 1.01 * algorithmic
+
+
+@pytest.mark.gpu
+def test_default_contract_on_one_gpu():
+    """A short run of the headline step (no sweep) prints one JSON line with every required key."""
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--no-sweep", "--steps", "2", "--warmup", "1"],
+                       capture_output=True, text=True, timeout=300, cwd=ROOT)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [line for line in r.stdout.splitlines() if line.strip()]
+    assert len(lines) == 1
+    out = json.loads(lines[0])
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+                "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
+        assert key in out, key
+    assert out["n_gpus"] == 1 and out["steps"] == 2 and out["warmup"] == 1 and out["unit"] == "TFLOP/s"
+    assert out["higher_is_better"] is True and out["vs_baseline"] is None and "workload" in out["config"]
+    roof = out["roofline"]
+    assert roof["bound"] == "mfma" and roof["unit"] == "TFLOP/s" and roof["peak"] == 2516.6
+    assert abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-9 and 0 < roof["frac"] < 1
+    assert roof["traffic"] is not None and roof["launches"] == 2 * 6
+    cpu = out["cpu_baseline"]
+    assert cpu["kind"] == "port" and cpu["cores"] >= 1 and cpu["value"] > 0 and cpu["sample"]
+    assert 0 < out["value"] < 2516.6

@@ -34,7 +34,8 @@ template <typename T, int D> struct FwdTable;
   TATTN_TABLE(NAME, _Float16, D, __VA_ARGS__) \
   TATTN_TABLE(NAME, __bf16, D, __VA_ARGS__)
 
-// Entry 0 of each table is the default pick. 16-bit forward entries and the 16-bit backward
+// The picks per sequence length are measured and live in pick_config (abi.hip); entry 0 is the
+// pick wherever no rule names another. 16-bit forward entries and the 16-bit backward
 // entries marked pipe run the software-pipelined kernels (32 rows per step). Every 16-bit
 // entry fits its register budget without scratch and can reach its waves per SIMD within the
 // 160 KB of LDS (a D=64 forward workgroup holds 44 KB of K/V ring); D=128 entries run at one

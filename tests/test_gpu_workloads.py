@@ -9,11 +9,14 @@ materialised attention and its autograd on the same seeded inputs.
 - Long context: B=1, H=16, N=16,384, D=64, inputs scaled by 0.5, causal and not; output and
   gradients, and the extra memory of forward + backward beyond inputs, outputs and gradients.
 - Strided inputs whose per-head slices span more than 2 GiB (the forward's 64-bit path).
+- One sequence of 65,536 tokens: O and M of the forward; one of 32,768 tokens: the gradients.
 - The reference bench's accuracy recipe at every length, held to the errors the reference
   published for its own kernels (tests/golden/t4_accuracy.json).
 
 Tolerances: fp16 |err| <= 2e-3 + 2e-3 |ref| (output and gradients), fp32 1e-5 + 1e-5 |ref|.
 The float32 reference is computed a few heads at a time so its N x N matrices stay near 1 GiB."""
+
+import math
 
 import pytest
 import torch
@@ -134,6 +137,62 @@ def test_forward_slices_beyond_2gib(causal):
     want = naive_attention(q.float(), k.float(), v.float(), causal=causal)
     torch.testing.assert_close(got.float(), want, **F16_TOL)
     del buf
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_forward_sequence_65536(causal):
+    """One sequence of 65,536 tokens (2 heads, D=64, fp16): O and M against float32 attention
+    computed 4,096 query rows at a time (row max and log-sum-exp in float32)."""
+    from tattn.api import _forward
+
+    n = 65536
+    g = torch.Generator(device=DEV).manual_seed(65536 + int(causal))
+    q, k, v = (torch.randn(1, 2, n, 64, device=DEV, dtype=torch.float16, generator=g) for _ in range(3))
+    o, m = _forward(q, k, v, causal, 0.125)
+    kf, vf = k.float(), v.float()
+    keys = torch.arange(n, device=DEV)
+    for s in range(0, n, 4096):
+        sc = (q[:, :, s:s + 4096].float() @ kf.transpose(-1, -2)) * 0.125
+        if causal:
+            sc = sc.masked_fill(keys[None, :] > torch.arange(s, s + 4096, device=DEV)[:, None], float("-inf"))
+        want_m = torch.logsumexp(sc, -1) / math.log(2.0)
+        want_o = torch.softmax(sc, -1) @ vf
+        torch.testing.assert_close(o[:, :, s:s + 4096].float(), want_o, **F16_TOL)
+        torch.testing.assert_close(m[:, :, s:s + 4096], want_m, atol=1e-3, rtol=1e-4)
+        del sc
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_sequence_32768(causal):
+    """One sequence of 32,768 tokens (1 head, D=64, fp16): dq, dk, dv against the float32
+    gradient formulas (P, dV = Pᵀ dO, dS = P(dO Vᵀ - δ), dQ = dS K s, dK = dSᵀ Q s) evaluated
+    2,048 query rows at a time."""
+    from tattn import attention
+
+    n, sc_ = 32768, 0.125
+    g = torch.Generator(device=DEV).manual_seed(32768 + int(causal))
+    q, k, v, do = (torch.randn(1, 1, n, 64, device=DEV, dtype=torch.float16, generator=g) for _ in range(4))
+    qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+    o = attention(qg, kg, vg, causal=causal)
+    o.backward(do)
+    qf, kf, vf, dof, of = (t[0, 0].float() for t in (q, k, v, do, o.detach()))
+    dq = torch.empty_like(qf)
+    dk = torch.zeros_like(kf)
+    dv = torch.zeros_like(vf)
+    keys = torch.arange(n, device=DEV)
+    for s in range(0, n, 2048):
+        sc = (qf[s:s + 2048] @ kf.T) * sc_
+        if causal:
+            sc = sc.masked_fill(keys[None, :] > torch.arange(s, s + 2048, device=DEV)[:, None], float("-inf"))
+        pr = torch.softmax(sc, -1)
+        delta = (dof[s:s + 2048] * of[s:s + 2048]).sum(-1, keepdim=True)
+        ds = pr * (dof[s:s + 2048] @ vf.T - delta)
+        dv += pr.T @ dof[s:s + 2048]
+        dk += ds.T @ qf[s:s + 2048] * sc_
+        dq[s:s + 2048] = ds @ kf * sc_
+        del sc, pr, ds
+    for name, got, want in (("dq", qg.grad, dq), ("dk", kg.grad, dk), ("dv", vg.grad, dv)):
+        torch.testing.assert_close(got[0, 0].float(), want, **F16_TOL, msg=lambda m: f"{name}: {m}")
 
 
 def _published():

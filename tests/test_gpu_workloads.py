@@ -5,7 +5,8 @@ materialised attention and its autograd on the same seeded inputs.
   batch 2, heads 3, q/k/v/dO made non-contiguous by transposing a [B, N, H, D] tensor to
   [B, H, N, D]; fp16 and fp32, causal and not; output and all three gradients.
 - Full size: fp16, H=16, D=64, B x N = 16,384 tokens at every N from 512 to 16,384, causal
-  and not, N(0,1) inputs; output and dq/dk/dv.
+  and not, N(0,1) inputs; output and dq/dk/dv. The same token count at N=4096 for head dim 128
+  (fp16, bf16) and for bf16 at head dim 64.
 - Long context: B=1, H=16, N=16,384, D=64, inputs scaled by 0.5, causal and not; output and
   gradients, and the extra memory of forward + backward beyond inputs, outputs and gradients.
 - Strided inputs whose per-head slices span more than 2 GiB (the forward's 64-bit path).
@@ -91,6 +92,21 @@ def test_full_size_fp16(n, causal):
     want = _reference(q, k, v, do, causal)
     for name, gt, w in zip(("o", "dq", "dk", "dv"), got, want):
         torch.testing.assert_close(gt, w, **F16_TOL, msg=lambda m: f"{name} n={n} causal={causal}: {m}")
+
+
+@pytest.mark.parametrize("d,dtype", [(128, torch.float16), (64, torch.bfloat16), (128, torch.bfloat16)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_other_head_dims_and_bf16_at_16k_tokens(d, dtype, causal):
+    """The benchmark's token count at N=4096 (B=4, H=16) for head dim 128 and for bfloat16:
+    output and gradients against float32 autograd. bf16 tolerance: the fp16 bound x 8 (bf16
+    carries 3 fewer mantissa bits)."""
+    g = torch.Generator(device=DEV).manual_seed(4096 + d + int(causal))
+    q, k, v, do = (torch.randn(4, 16, 4096, d, device=DEV, dtype=dtype, generator=g) for _ in range(4))
+    got = _run(q, k, v, do, causal)
+    want = _reference(q, k, v, do, causal)
+    tol = F16_TOL if dtype == torch.float16 else {"atol": 1.6e-2, "rtol": 1.6e-2}
+    for name, gt, w in zip(("o", "dq", "dk", "dv"), got, want):
+        torch.testing.assert_close(gt, w, **tol, msg=lambda m: f"{name} d={d} {dtype} causal={causal}: {m}")
 
 
 @pytest.mark.parametrize("causal", [False, True])

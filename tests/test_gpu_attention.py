@@ -83,6 +83,31 @@ def test_custom_scale_and_noncontiguous_inputs():
     torch.testing.assert_close(got, naive_attention(q, k, v, sm_scale=0.3), **F32_TOL)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_three_different_layouts(dtype, causal):
+    """q contiguous, k from a [B, N, H, D] buffer, v from an [N, B, H, D] buffer: the forward reads
+    each through its own strides (no copies), the backward makes them contiguous."""
+    from tattn import attention
+
+    b_, h, n, d = 2, 4, 300, 64
+    q = r((b_, h, n, d), dtype, 800)
+    k = r((b_, n, h, d), dtype, 801).transpose(1, 2)
+    v = r((n, b_, h, d), dtype, 802).permute(1, 2, 0, 3)
+    do = r((b_, h, n, d), dtype, 803)
+    assert len({q.stride(), k.stride(), v.stride()}) == 3
+    qs, ks, vs = (t.clone().requires_grad_() for t in (q, k, v))  # clone keeps the strides
+    assert ks.stride() == k.stride() and vs.stride() == v.stride()
+    out = attention(qs, ks, vs, causal=causal)
+    out.backward(do)
+    qr, kr, vr = (t.float().requires_grad_() for t in (q, k, v))
+    ref = naive_attention(qr, kr, vr, causal=causal)
+    ref.backward(do.float())
+    for name, got, want in zip(("o", "dq", "dk", "dv"), (out, qs.grad, ks.grad, vs.grad),
+                               (ref, qr.grad, kr.grad, vr.grad)):
+        torch.testing.assert_close(got.float(), want.detach(), **tol(dtype), msg=lambda m: f"{name}: {m}")
+
+
 def test_backward_with_noncontiguous_inputs_and_grad():
     from tattn import attention
 

@@ -108,6 +108,25 @@ def test_three_different_layouts(dtype, causal):
         torch.testing.assert_close(got.float(), want.detach(), **tol(dtype), msg=lambda m: f"{name}: {m}")
 
 
+@pytest.mark.parametrize("offset", [1, 3, 8])
+def test_unaligned_views(offset):
+    """Views starting `offset` fp16 elements into a buffer (2 or 6 bytes: not 16-byte aligned,
+    copied before the launch; 16 bytes: aligned, read in place) and rows of 72 elements."""
+    from tattn import attention
+
+    b_, h, n, d = 1, 2, 100, 64
+    views = []
+    for i in range(3):
+        buf = r((b_ * h * n * 72 + offset,), torch.float16, 900 + i)
+        views.append(buf[offset:].view(b_, h, n, 72)[..., :d])
+    q, k, v = views
+    assert (q.data_ptr() % 16 == 0) == (offset * 2 % 16 == 0) and q.stride(2) == 72
+    for causal in (False, True):
+        got = attention(q, k, v, causal=causal)
+        want = naive_attention(q.float(), k.float(), v.float(), causal=causal)
+        torch.testing.assert_close(got.float(), want, **F16_TOL)
+
+
 def test_backward_with_noncontiguous_inputs_and_grad():
     from tattn import attention
 

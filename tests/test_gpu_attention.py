@@ -350,6 +350,44 @@ def test_graph_capture_and_replay(causal):
             assert torch.equal(got, want), (rep, name)
 
 
+def test_concurrent_threads_on_their_own_streams():
+    """Two host threads, each with its own stream, run forward + backward at once: each gets the
+    single-threaded result's bits (no shared state in the library beyond read-only tables)."""
+    import threading
+
+    from tattn import attention
+
+    inputs = [[r((2, 4, 257, 64), torch.float16, 1000 + 10 * t + s) for s in range(4)] for t in range(2)]
+
+    def run(q, k, v, do):
+        qg, kg, vg = (x.clone().requires_grad_() for x in (q, k, v))
+        out = attention(qg, kg, vg, causal=True)
+        out.backward(do)
+        return [out.detach(), qg.grad, kg.grad, vg.grad]
+
+    want = [run(*x) for x in inputs]
+    torch.cuda.synchronize()
+    got = [None, None]
+
+    def worker(t):
+        stream = torch.cuda.Stream()
+        with torch.cuda.stream(stream):
+            for _ in range(5):
+                res = run(*inputs[t])
+            stream.synchronize()
+        got[t] = res
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    for t in range(2):
+        assert got[t] is not None
+        for a_, b_ in zip(got[t], want[t]):
+            assert torch.equal(a_, b_)
+
+
 def test_uses_current_stream():
     """Work is enqueued on the caller's current stream (no host sync inside the call)."""
     from tattn import attention

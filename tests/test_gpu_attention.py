@@ -47,6 +47,7 @@ def r(shape, dtype, seed):
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_forward_matches_definition(shape, causal, dtype):
+    """tests/test_attention.py:30-40 (the reference's shapes; tighter tolerance here)."""
     from tattn import attention
 
     q, k, v = (r(shape, dtype, s) for s in (1, 2, 3))
@@ -60,6 +61,7 @@ def test_forward_matches_definition(shape, causal, dtype):
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_gradients_match_autograd(shape, causal, dtype):
+    """tests/test_attention.py:43-54 (gradients against float32 autograd of the definition)."""
     from tattn import attention
 
     q, k, v = (r(shape, dtype, s).requires_grad_() for s in (4, 5, 6))
@@ -73,6 +75,7 @@ def test_gradients_match_autograd(shape, causal, dtype):
 
 
 def test_custom_scale_and_noncontiguous_inputs():
+    """tests/test_attention.py:57-64."""
     from tattn import attention
 
     q = r((1, 20, 2, 32), torch.float32, 9).transpose(1, 2)
@@ -128,6 +131,7 @@ def test_unaligned_views(offset):
 
 
 def test_backward_with_noncontiguous_inputs_and_grad():
+    """tests/test_attention.py:107-114."""
     from tattn import attention
 
     q, k, v, do = (r((1, 21, 2, 16), torch.float32, s).transpose(1, 2) for s in (20, 21, 22, 23))
@@ -141,6 +145,7 @@ def test_backward_with_noncontiguous_inputs_and_grad():
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_head_dim_128(causal):
+    """tests/test_attention.py:117-124, for both masks."""
     from tattn import attention
 
     q, k, v = (r((1, 1, 19, 128), torch.float16, s).requires_grad_() for s in (30, 31, 32))
@@ -157,6 +162,7 @@ def test_head_dim_128(causal):
 
 
 def test_double_backward_is_refused_not_wrong():
+    """tests/test_attention.py:127-131."""
     from tattn import attention
 
     q, k, v = (r((1, 1, 8, 16), torch.float32, s).requires_grad_() for s in (40, 41, 42))
@@ -166,6 +172,7 @@ def test_double_backward_is_refused_not_wrong():
 
 
 def test_backend_selection():
+    """tests/test_attention.py:93-104 (`triton_available` kept as the backend probe)."""
     from tattn import hip_available, triton_available
 
     assert triton_available(DEV) and hip_available(DEV)

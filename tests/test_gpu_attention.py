@@ -130,6 +130,39 @@ def test_unaligned_views(offset):
         torch.testing.assert_close(got.float(), want, **F16_TOL)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("scale", [-0.125, -1.0, 0.0, 1.0])
+def test_any_softmax_scale(dtype, scale):
+    """sm_scale is any float in the reference (scores are multiplied by it before the row max is
+    taken, kernels.py:115, 127-132): negative, zero and large scales. Output against float32
+    attention; gradients against float32 autograd (fp32) or, for 16-bit inputs, against the
+    backward with the reference kernels' rounding points (large scales give near one-hot rows,
+    where the rounding of the stored O dominates, as in the softmax stress test)."""
+    from tattn.api import _backward, _forward
+
+    q, k, v, do = (r((2, 3, 150, 64), dtype, 1100 + s) for s in range(4))
+    t = tol(dtype)
+    for causal in (False, True):
+        o, m = _forward(q, k, v, causal, scale)
+        assert torch.isfinite(o).all() and torch.isfinite(m).all()
+        ref = naive_attention(q.float(), k.float(), v.float(), causal=causal, sm_scale=scale)
+        torch.testing.assert_close(o.float(), ref, **t, msg=lambda msg: f"o causal={causal}: {msg}")
+        got = _backward(q, k, v, o, m, do, causal, scale)
+        if dtype == torch.float32:
+            qr, kr, vr = (x.detach().float().clone().requires_grad_() for x in (q, k, v))
+            naive_attention(qr, kr, vr, causal=causal, sm_scale=scale).backward(do.float())
+            # Rounding of the scaled scores grows with |scale| (and dq, dk carry one more factor of
+            # it), so the fp32 envelope (set at the default 1/8) is scaled with |scale| / (1/8).
+            g_tol = {key: val * max(1.0, abs(scale) / 0.125) for key, val in t.items()}
+            for name, g_, w in zip(("dq", "dk", "dv"), got, (qr.grad, kr.grad, vr.grad)):
+                torch.testing.assert_close(g_, w, **g_tol, msg=lambda msg: f"{name} causal={causal}: {msg}")
+        else:
+            want, flips = _emulated_backward(q, k, v, o, m, do, causal, scale)
+            for name, g_, w, bnd in zip(("dq", "dk", "dv"), got, want, flips):
+                excess = ((g_.float() - w).abs() - t["atol"] - t["rtol"] * w.abs() - bnd).max().item()
+                assert excess <= 0, f"{name} causal={causal}: error exceeds the bound by {excess:.3e}"
+
+
 def test_backward_with_noncontiguous_inputs_and_grad():
     """tests/test_attention.py:107-114."""
     from tattn import attention
@@ -465,7 +498,7 @@ def _emulated_backward(q, k, v, o, m, do, causal, scale):
     float32 on materialised matrices: delta from the stored (rounded) O, P = exp2(S c - M) from
     the saved M, P and dS rounded to the input dtype before the products that use them.
     Returns (dq, dk, dv) and, per element, the change that one-ulp flips of those rounded
-    operands can cause (2u sum |dS||K| scale, 2u sum |dS||Q| scale, 2u sum |P||dO|): a last-bit
+    operands can cause (2u sum |dS||K| |scale|, 2u sum |dS||Q| |scale|, 2u sum |P||dO|): a last-bit
     difference upstream (summation order of S) may move a value across a rounding boundary."""
     dt = q.dtype
     qf, kf, vf, dof = (t.float() for t in (q, k, v, do))
@@ -482,8 +515,8 @@ def _emulated_backward(q, k, v, o, m, do, causal, scale):
     dq = ds @ kf * scale
     dk = ds.transpose(-1, -2).contiguous() @ qf * scale
     two_u = 2.0 ** -10 if dt == torch.float16 else 2.0 ** -7
-    bq = two_u * scale * (ds.abs() @ kf.abs())
-    bk = two_u * scale * (ds.abs().transpose(-1, -2).contiguous() @ qf.abs())
+    bq = two_u * abs(scale) * (ds.abs() @ kf.abs())
+    bk = two_u * abs(scale) * (ds.abs().transpose(-1, -2).contiguous() @ qf.abs())
     bv = two_u * (p.transpose(-1, -2).contiguous() @ dof.abs())
     return (dq, dk, dv), (bq, bk, bv)
 

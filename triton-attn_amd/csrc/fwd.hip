@@ -152,32 +152,31 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_generic_kernel(const FwdPara
         for (int j = 0; j < QT; ++j) s[t][j] = E::mfma(kop, qop[j][sd], s[t][j]);
       }
     }
-    if constexpr (MASK) {
+    // Hidden keys: excluded from the max of the scaled scores (the scale may be negative or
+    // zero) and given probability 0 after the exponential.
+    bool dead[C::KT][QT][16];
 #pragma unroll
-      for (int t = 0; t < C::KT; ++t)
+    for (int t = 0; t < C::KT; ++t)
 #pragma unroll
-        for (int j = 0; j < QT; ++j) {
-          const int q = qw0 + 32 * j + l32;
+      for (int j = 0; j < QT; ++j) {
+        const int q = qw0 + 32 * j + l32;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kb + 32 * t + kappa(r, h2);
-            const bool dead = key >= N || (CAUSAL && key > q);
-            s[t][j][r] = dead ? -__builtin_inff() : s[t][j][r];
-          }
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb + 32 * t + kappa(r, h2);
+          dead[t][j][r] = MASK && (key >= N || (CAUSAL && key > q));
         }
-    }
+      }
     // Row max of every q-tile first, then one wave-uniform rescale branch for the whole step.
     float mnew[QT], alpha[QT];
     bool any_upd = false;
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
-      float mx = s[0][j][0];
+      float mx = -__builtin_inff();
 #pragma unroll
       for (int t = 0; t < C::KT; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, s[t][j][r]);
-      mx = max_halves(mx);
-      const float cand = mx * c;
+        for (int r = 0; r < 16; ++r) mx = dead[t][j][r] ? mx : __builtin_fmaxf(mx, s[t][j][r] * c);
+      const float cand = max_halves(mx);
       const bool upd = cand > mrow[j] + kRescaleLog2;
       mnew[j] = upd ? cand : mrow[j];
       alpha[j] = fast_exp2(mrow[j] - mnew[j]);
@@ -199,7 +198,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_generic_kernel(const FwdPara
       for (int t = 0; t < C::KT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float e = fast_exp2(__builtin_fmaf(s[t][j][r], c, nm));
+          const float e = dead[t][j][r] ? 0.0f : fast_exp2(__builtin_fmaf(s[t][j][r], c, nm));
           s[t][j][r] = e;
           ps[r & 3] = (t == 0 && r < 4) ? e : ps[r & 3] + e;
         }
@@ -487,27 +486,28 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
 
   // Softmax of scur (keys kb..kb+31): probabilities into pc, running max and sum updated;
   // returns whether any row of the wave raised its max (the accumulator then needs alpha).
+  // The max is taken over the scaled scores (the scale may be negative or zero) and hidden keys
+  // get probability 0 after the exponential; for a positive scale this is the same max and the
+  // same probabilities as scaling the max of the raw scores.
   auto softmax = [&](f32x16* scur, V8 (*pc)[2], float* alpha, int kb, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
-    if constexpr (MASK) {
+    bool dead[QT][16];
 #pragma unroll
-      for (int j = 0; j < QT; ++j) {
-        const int q = qw0 + 32 * j + l32;
+    for (int j = 0; j < QT; ++j) {
+      const int q = qw0 + 32 * j + l32;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kb + kappa(r, h2);
-          scur[j][r] = (key >= N || (CAUSAL && key > q)) ? -__builtin_inff() : scur[j][r];
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb + kappa(r, h2);
+        dead[j][r] = MASK && (key >= N || (CAUSAL && key > q));
       }
     }
     bool any_upd = false;
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
-      float mx = __builtin_fmaxf(scur[j][0], scur[j][1]);
+      float mx = -__builtin_inff();
 #pragma unroll
-      for (int r = 2; r < 16; ++r) mx = __builtin_fmaxf(mx, scur[j][r]);
-      mx = max_halves(mx);
-      const float cand = mx * c;
+      for (int r = 0; r < 16; ++r) mx = dead[j][r] ? mx : __builtin_fmaxf(mx, scur[j][r] * c);
+      const float cand = max_halves(mx);
       const bool upd = cand > mrow[j] + kRescaleLog2;
       const float mnew = upd ? cand : mrow[j];
       alpha[j] = fast_exp2(mrow[j] - mnew);
@@ -520,8 +520,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
         V8 x;
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
-          const float e0 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i], c, nm));
-          const float e1 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i + 1], c, nm));
+          float e0 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i], c, nm));
+          float e1 = fast_exp2(__builtin_fmaf(scur[j][8 * sg + i + 1], c, nm));
+          e0 = dead[j][8 * sg + i] ? 0.0f : e0;
+          e1 = dead[j][8 * sg + i + 1] ? 0.0f : e1;
           const V2 pr = H::pack(e0, e1);
           ps = H::sum2(pr, ps);
           x[i] = pr[0];
@@ -651,9 +653,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kappa(r, h2);
-        mx = (key < N && (!CAUSAL || key <= q)) ? __builtin_fmaxf(mx, sa[j][r]) : mx;
+        mx = (key < N && (!CAUSAL || key <= q)) ? __builtin_fmaxf(mx, sa[j][r] * c) : mx;
       }
-      mrow[j] = max_halves(mx) * c;
+      mrow[j] = max_halves(mx);
     }
   }
 

@@ -131,7 +131,7 @@ def test_unaligned_views(offset):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("scale", [-0.125, -1.0, 0.0, 1.0])
+@pytest.mark.parametrize("scale", [-0.125, -1.0, 0.0, 1.0, 8.0])
 def test_any_softmax_scale(dtype, scale):
     """sm_scale is any float in the reference (scores are multiplied by it before the row max is
     taken, kernels.py:115, 127-132): negative, zero and large scales. Output against float32
@@ -142,20 +142,21 @@ def test_any_softmax_scale(dtype, scale):
 
     q, k, v, do = (r((2, 3, 150, 64), dtype, 1100 + s) for s in range(4))
     t = tol(dtype)
+    # fp32: rounding of the scaled scores grows with |scale| (dq and dk carry one more factor of
+    # it), so the fp32 envelope, set at the default 1/8, is scaled by |scale| / (1/8).
+    t32 = {key: val * max(1.0, abs(scale) / 0.125) for key, val in t.items()}
     for causal in (False, True):
         o, m = _forward(q, k, v, causal, scale)
         assert torch.isfinite(o).all() and torch.isfinite(m).all()
         ref = naive_attention(q.float(), k.float(), v.float(), causal=causal, sm_scale=scale)
-        torch.testing.assert_close(o.float(), ref, **t, msg=lambda msg: f"o causal={causal}: {msg}")
+        torch.testing.assert_close(o.float(), ref, **(t32 if dtype == torch.float32 else t),
+                                   msg=lambda msg: f"o causal={causal}: {msg}")
         got = _backward(q, k, v, o, m, do, causal, scale)
         if dtype == torch.float32:
             qr, kr, vr = (x.detach().float().clone().requires_grad_() for x in (q, k, v))
             naive_attention(qr, kr, vr, causal=causal, sm_scale=scale).backward(do.float())
-            # Rounding of the scaled scores grows with |scale| (and dq, dk carry one more factor of
-            # it), so the fp32 envelope (set at the default 1/8) is scaled with |scale| / (1/8).
-            g_tol = {key: val * max(1.0, abs(scale) / 0.125) for key, val in t.items()}
             for name, g_, w in zip(("dq", "dk", "dv"), got, (qr.grad, kr.grad, vr.grad)):
-                torch.testing.assert_close(g_, w, **g_tol, msg=lambda msg: f"{name} causal={causal}: {msg}")
+                torch.testing.assert_close(g_, w, **t32, msg=lambda msg: f"{name} causal={causal}: {msg}")
         else:
             want, flips = _emulated_backward(q, k, v, o, m, do, causal, scale)
             for name, g_, w, bnd in zip(("dq", "dk", "dv"), got, want, flips):

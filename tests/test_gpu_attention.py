@@ -164,6 +164,35 @@ def test_any_softmax_scale(dtype, scale):
                 assert excess <= 0, f"{name} causal={causal}: error exceeds the bound by {excess:.3e}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_broadcast_key_value_views(dtype):
+    """K and V shared by every head and batch through expand() (stride 0, the multi-query
+    layout): the forward reads them in place, and the gradients of the shared tensors come back
+    summed over the broadcast dimensions by autograd."""
+    from tattn import attention
+
+    q = r((2, 4, 90, 64), dtype, 1200).requires_grad_()
+    k1 = r((1, 1, 90, 64), dtype, 1201).requires_grad_()
+    v1 = r((1, 1, 90, 64), dtype, 1202).requires_grad_()
+    do = r((2, 4, 90, 64), dtype, 1203)
+    k, v = k1.expand(2, 4, 90, 64), v1.expand(2, 4, 90, 64)
+    assert k.stride()[:2] == (0, 0)
+    for causal in (False, True):
+        q.grad = k1.grad = v1.grad = None
+        out = attention(q, k, v, causal=causal)
+        out.backward(do)
+        qr, k1r, v1r = (x.detach().float().clone().requires_grad_() for x in (q, k1, v1))
+        ref = naive_attention(qr, k1r.expand(2, 4, 90, 64), v1r.expand(2, 4, 90, 64), causal=causal)
+        ref.backward(do.float())
+        t = tol(dtype)
+        torch.testing.assert_close(out.float(), ref.detach(), **t)
+        for name, got, want in (("dq", q.grad, qr.grad), ("dk", k1.grad, k1r.grad), ("dv", v1.grad, v1r.grad)):
+            # dk and dv sum 8 heads' gradients: the envelope grows with the number of terms
+            scale = 8.0 if name != "dq" else 1.0
+            torch.testing.assert_close(got.float(), want, atol=t["atol"] * scale, rtol=t["rtol"] * scale,
+                                       msg=lambda m: f"{name} causal={causal}: {m}")
+
+
 def test_backward_with_noncontiguous_inputs_and_grad():
     """tests/test_attention.py:107-114."""
     from tattn import attention

@@ -215,7 +215,9 @@ def derived(cs: dict[str, float]) -> dict[str, float]:
     mfma_busy: MFMA-busy SIMD cycles per SIMD cycle of the CUs' busy time (4 SIMDs per CU);
     lds_bank_conflict_per_lds_cycle: bank-conflict cycles per cycle with an LDS instruction active;
     valu_per_mfma: VALU instructions per MFMA instruction;
-    lds_load_bytes: LDS read bytes (SQ_INSTS_LDS_LOAD_BANDWIDTH counts 64-byte units)."""
+    lds_load_bytes: LDS read bytes (SQ_INSTS_LDS_LOAD_BANDWIDTH counts 64-byte units);
+    lds_bytes_per_cu_cycle: those bytes per busy CU cycle (a CU's LDS returns at most 128 B per
+    cycle: one ds_read_b128 of a wave64 takes 8 cycles)."""
     out: dict[str, float] = {}
     if cs.get("SQ_BUSY_CU_CYCLES") and "SQ_VALU_MFMA_BUSY_CYCLES" in cs:
         out["mfma_busy"] = cs["SQ_VALU_MFMA_BUSY_CYCLES"] / (4 * cs["SQ_BUSY_CU_CYCLES"])
@@ -225,6 +227,8 @@ def derived(cs: dict[str, float]) -> dict[str, float]:
         out["valu_per_mfma"] = cs["SQ_INSTS_VALU"] / cs["SQ_INSTS_MFMA"]
     if "SQ_INSTS_LDS_LOAD_BANDWIDTH" in cs:
         out["lds_load_bytes"] = cs["SQ_INSTS_LDS_LOAD_BANDWIDTH"] * 64
+        if cs.get("SQ_BUSY_CU_CYCLES"):
+            out["lds_bytes_per_cu_cycle"] = out["lds_load_bytes"] / cs["SQ_BUSY_CU_CYCLES"]
     return out
 
 

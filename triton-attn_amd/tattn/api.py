@@ -120,7 +120,7 @@ def _stream(t: torch.Tensor) -> int:
 # the caller's stream (HIP events; skipped while a graph is being captured) and keeps the
 # fastest for that key.
 _autotune = os.environ.get("TATTN_AUTOTUNE", "0") not in ("", "0")
-_tuned: dict[tuple[int, int, int, int, bool, int], int] = {}
+_tuned: dict[tuple[int, int, int, int, int, bool], int] = {}  # (kernel, device, N bucket, D, dtype, causal)
 
 
 def set_autotune(on: bool) -> None:

@@ -327,12 +327,13 @@ def test_zero_queries_give_mean_and_cumulative_mean():
     torch.testing.assert_close(attention(q, k, v, causal=True), v.cumsum(-2) / cnt, **F32_TOL)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("causal", [False, True])
-def test_run_to_run_bitwise_identical(causal):
+def test_run_to_run_bitwise_identical(causal, dtype):
     """No atomics anywhere: two runs give the same bits."""
     from tattn.api import _backward, _forward
 
-    q, k, v, do = (r((2, 4, 777, 64), torch.float16, s) for s in (80, 81, 82, 83))
+    q, k, v, do = (r((2, 4, 777, 64), dtype, s) for s in (80, 81, 82, 83))
     o1, m1 = _forward(q, k, v, causal, 0.125)
     o2, m2 = _forward(q, k, v, causal, 0.125)
     assert torch.equal(o1, o2) and torch.equal(m1, m2)

@@ -225,6 +225,21 @@ def test_head_dim_128(causal):
         torch.testing.assert_close(g.float(), w, **F16_TOL)
 
 
+def test_retained_graph_backward_twice_accumulates():
+    """backward(retain_graph=True) twice: the saved q, k, v, O, M are reused and the leaf
+    gradients accumulate to exactly twice one backward (same bits, doubled)."""
+    from tattn import attention
+
+    q, k, v = (r((1, 2, 130, 64), torch.float16, 1300 + s).requires_grad_() for s in range(3))
+    do = r((1, 2, 130, 64), torch.float16, 1303)
+    out = attention(q, k, v, causal=True)
+    out.backward(do, retain_graph=True)
+    once = [t.grad.clone() for t in (q, k, v)]
+    out.backward(do)
+    for t, g1 in zip((q, k, v), once):
+        assert torch.equal(t.grad, g1 + g1)
+
+
 def test_double_backward_is_refused_not_wrong():
     """tests/test_attention.py:127-131."""
     from tattn import attention

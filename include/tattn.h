@@ -112,6 +112,20 @@ int tattn_bwd(const void* q, const void* k, const void* v, const void* o, const 
               int dtype, int causal, float sm_scale, int config_id, void* stream);
 
 /*
+ * tattn_bwd without the delta argument and without any allocation: delta lives in a static
+ * device array of the library (16 MiB per GPU, held until the process ends), so the caller
+ * passes only inputs and outputs. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Limit: Z*H*N <= 4,194,304 query rows, else TATTN_E_ARG and nothing
+ * is enqueued. Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (two streams, two threads) race on it and must be serialised by the caller.
+ */
+int tattn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                      void* dq, void* dk, void* dv, const float* m,
+                      const int64_t strides[4], int64_t Z, int64_t H, int64_t N, int64_t D,
+                      int dtype, int causal, float sm_scale, int config_id, void* stream);
+
+/*
  * Tile table introspection (the gfx950 replacement of the reference's autotune config lists,
  * src/tattn/kernels.py:21-54): number of entries for (kernel, D, dtype), the entry itself, and
  * the entry the library picks for a problem (the reference keys its autotuner on

@@ -93,3 +93,11 @@ def test_bwd_rejects_bad_config_for_both_tables():
     rc = lib.tattn_bwd(16, 16, 16, 16, 16, 16, 16, 16, 16, 16, st, 1, 1, 16, 64, _lib.F16, 0,
                        0.125, 99, None)
     assert rc == 2 and "out of range" in _lib.last_error()
+
+
+def test_bwd_noalloc_rejects_problems_past_its_workspace_before_launch():
+    lib = _lib.load()
+    st = (ctypes.c_int64 * 4)(1 << 20, 1 << 16, 64, 1)
+    rc = lib.tattn_bwd_noalloc(16, 16, 16, 16, 16, 16, 16, 16, 16, st, 1, 65, 1 << 16, 64, _lib.F16, 0,
+                               0.125, -1, None)
+    assert rc == 1 and "exceeds the static workspace" in _lib.last_error()

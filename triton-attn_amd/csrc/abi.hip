@@ -121,6 +121,36 @@ int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N) {
   return 0;
 }
 
+// Workspace of tattn_bwd_noalloc: the backward's delta (float32, one value per query row) in a
+// fixed device array, so that entry point needs neither an allocation nor a caller-provided
+// buffer. Every GPU holds its own copy (16 MiB) until the process ends. Host code must never
+// pass `scratch` itself to a kernel or copy: that name is a host-side stand-in, not a device
+// address. The device address is looked up once per device with hipGetSymbolAddress (with that
+// device current) and kept in g_scratch_ptr.
+constexpr int64_t kScratchRows = int64_t(1) << 22;  // Z * H * N <= 4,194,304
+static __device__ __align__(256) float scratch[kScratchRows];
+
+std::once_flag g_scratch_once[kMaxDevices];
+float* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// Device address of this device's scratch array (the current device; device_check has run).
+int scratch_for_current_device(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(TATTN_E_DEVICE, "hipGetDevice failed: %s", hipGetErrorString(e));
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* ptr = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? static_cast<float*>(ptr) : nullptr;
+  });
+  if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev])
+    return set_error(TATTN_E_DEVICE, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                     hipGetErrorString(g_scratch_err[dev]));
+  *out = g_scratch_ptr[dev];
+  return TATTN_OK;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int check_tensor(const char* name, const void* ptr, const int64_t* st, int sz) {
@@ -298,6 +328,24 @@ int tattn_bwd(const void* q, const void* k, const void* v, const void* o, const 
                            stream)))
     return rc;
   return tattn_bwd_dq(q, k, v, dout, dq, m, delta, strides, Z, H, N, D, dtype, causal, sm_scale, dq_id, stream);
+}
+
+int tattn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o, const void* dout, void* dq,
+                      void* dk, void* dv, const float* m, const int64_t strides[4], int64_t Z, int64_t H,
+                      int64_t N, int64_t D, int dtype, int causal, float sm_scale, int config_id, void* stream) {
+  int rc;
+  if ((rc = check_shape(Z, H, N, D, dtype))) return rc;
+  if (Z * H * N > kScratchRows)
+    return set_error(TATTN_E_ARG,
+                     "tattn_bwd_noalloc: Z*H*N = %lld query rows exceeds the static workspace of %lld rows; "
+                     "use tattn_bwd with a caller-provided delta",
+                     (long long)(Z * H * N), (long long)kScratchRows);
+  if ((rc = device_check())) return rc;
+  float* delta = nullptr;
+  if ((rc = scratch_for_current_device(&delta))) return rc;
+  // delta is written in full by the preprocess before dK/dV and dQ read it: nothing to clear.
+  return tattn_bwd(q, k, v, o, dout, dq, dk, dv, m, delta, strides, Z, H, N, D, dtype, causal, sm_scale,
+                   config_id, stream);
 }
 
 }  // extern "C"

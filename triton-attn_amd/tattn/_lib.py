@@ -22,8 +22,8 @@ KERNEL_NAMES = {K_FWD: "fwd", K_BWD_DKDV: "bwd_dkdv", K_BWD_DQ: "bwd_dq"}
 # Every symbol include/tattn.h declares.
 EXPORTS = (
     "tattn_abi_version", "tattn_last_error", "tattn_device_supported", "tattn_fwd",
-    "tattn_bwd_preprocess", "tattn_bwd_dkdv", "tattn_bwd_dq", "tattn_bwd", "tattn_num_configs",
-    "tattn_config_desc", "tattn_pick_config",
+    "tattn_bwd_preprocess", "tattn_bwd_dkdv", "tattn_bwd_dq", "tattn_bwd", "tattn_bwd_noalloc",
+    "tattn_num_configs", "tattn_config_desc", "tattn_pick_config",
 )
 
 
@@ -53,6 +53,7 @@ _SIGS = {
     "tattn_bwd_dkdv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _STR4, _I64, _I64, _I64, _I64, _I, _I, _F, _I, _P]),
     "tattn_bwd_dq": (_I, [_P, _P, _P, _P, _P, _P, _P, _STR4, _I64, _I64, _I64, _I64, _I, _I, _F, _I, _P]),
     "tattn_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _STR4, _I64, _I64, _I64, _I64, _I, _I, _F, _I, _P]),
+    "tattn_bwd_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _STR4, _I64, _I64, _I64, _I64, _I, _I, _F, _I, _P]),
     "tattn_num_configs": (_I, [_I, _I64, _I]),
     "tattn_config_desc": (_I, [_I, _I64, _I, _I, ctypes.POINTER(TattnConfig)]),
     "tattn_pick_config": (_I, [_I, _I64, _I, _I, _I64]),

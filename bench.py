@@ -11,10 +11,12 @@ step's counted flops divided by its time. The same line carries the roofline of 
 kernel (HIP events around every forward launch of the timed steps, on the launch stream), the
 per-N sweep (forward, causal and non-causal; fwd+bwd, causal and non-causal, with peak extra
 memory) timed like the reference's tables (tattn.timing.do_bench: cache flushed before each
-call, median over ~100 ms), and a CPU baseline: the oracle's tiled forward timed on the host
-cores on a bounded sample.
+call, median over ~100 ms), the accuracy of each shape as the reference's benchmark measures it
+(bench/bench.py:128-171: forward max / mean abs error against float32 attention at every N and
+both masks, dq/dk/dv max abs error against float32 autograd at N = 1024 and 4096), and a CPU
+baseline: the oracle's tiled forward timed on the host cores on a bounded sample.
 
-Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline] [--no-accuracy]
 """
 
 from __future__ import annotations
@@ -72,13 +74,24 @@ def measured_traffic() -> int | None:
     return None
 
 
+def cpu_threads() -> tuple[int, int, str]:
+    """(cores this process may run on, threads to use, why they differ). The thread count is the
+    host's per-process thread budget when one is set (OMP_NUM_THREADS: a GPU box gives each GPU a
+    share of its cores), else every core of the affinity mask."""
+    cores = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and 0 < int(env) < cores:
+        return cores, int(env), f"OMP_NUM_THREADS={env}: the host's thread budget for this process"
+    return cores, cores, "every core of the affinity mask"
+
+
 def cpu_baseline() -> dict:
     """The oracle's tiled forward (restatement of the reference's CPU path) on the host CPU."""
     import torch
 
     from oracle.reference import tiled_forward
 
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    affinity, threads, why = cpu_threads()
     torch.set_num_threads(threads)
     b, h, n, d = 1, 4, 8192, DIM
     g = torch.Generator().manual_seed(8192)
@@ -95,10 +108,59 @@ def cpu_baseline() -> dict:
         "value": flops(b, h, n, d, False, "fwd") / sec / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
+        "threads": threads,
+        "affinity_cores": affinity,
+        "thread_choice": why,
         "kind": "port",
         "sample": f"oracle tiled_forward (fp32 math on fp16 inputs), [B={b},H={h},N={n},D={d}] non-causal, "
                   f"128x128 blocks, median of 3 after 1 warm-up, {sec:.3f} s per run",
     }
+
+
+def _reference_out(q, k, v, causal):
+    """float32 materialised attention, a few heads at a time (~1 GiB of scores per chunk)."""
+    import torch
+
+    from oracle.reference import naive_attention
+
+    z, h, n, _ = q.shape
+    per = max(1, (1 << 28) // (z * n * n))
+    return torch.cat([naive_attention(q[:, i:i + per].float(), k[:, i:i + per].float(), v[:, i:i + per].float(),
+                                      causal=causal) for i in range(0, h, per)], dim=1)
+
+
+def accuracy(data) -> list[dict]:
+    """The reference benchmark's accuracy recipe (bench/bench.py:128-171) on the benchmark's own
+    inputs: forward max / mean abs error against float32 attention for every N and mask (all
+    heads up to N = 4096, the first two heads of batch 0 beyond); dq, dk, dv max abs error
+    against float32 autograd on batch 0 at N = 1024 and 4096 (dO from the same generator)."""
+    import torch
+
+    from oracle.reference import naive_attention
+    from tattn import attention
+
+    rows = []
+    for causal in (False, True):
+        for n in SEQS:
+            _, q, k, v, do = data[n]
+            if n > 4096:
+                q, k, v = (t[:1, :2].contiguous() for t in (q, k, v))
+            with torch.inference_mode():
+                err = (attention(q, k, v, causal=causal).float() - _reference_out(q, k, v, causal)).abs()
+            rows.append({"seq": n, "causal": causal, "what": "o", "max_abs_err": float(f"{err.max().item():.4g}"),
+                         "mean_abs_err": float(f"{err.mean().item():.4g}")})
+            del err
+        for n in (1024, 4096):
+            _, q, k, v, do = data[n]
+            q, k, v, do = (t[:1].clone() for t in (q, k, v, do))
+            qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+            attention(qg, kg, vg, causal=causal).backward(do)
+            qr, kr, vr = (t.float().requires_grad_() for t in (q, k, v))
+            naive_attention(qr, kr, vr, causal=causal).backward(do.float())
+            for name, got, want in (("dq", qg.grad, qr.grad), ("dk", kg.grad, kr.grad), ("dv", vg.grad, vr.grad)):
+                rows.append({"seq": n, "causal": causal, "what": name,
+                             "max_abs_err": float(f"{(got.float() - want).abs().max().item():.4g}")})
+    return rows
 
 
 def main() -> int:
@@ -107,6 +169,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-accuracy", action="store_true", help="skip the per-shape error measurement")
     ap.add_argument("--no-sweep", action="store_true", help="only the headline forward step")
     ap.add_argument("--seqs", default=",".join(map(str, SEQS)),
                     help="sequence lengths of the step (16,384 tokens each); default: all six")
@@ -203,11 +266,23 @@ def main() -> int:
     traffic = None
     if seqs == SEQS and not a.causal:
         traffic = measured_traffic()
+    # Per shape: the table entry the forward runs, its average launch time and roofline fraction.
+    from tattn import _lib
+
+    per_n = []
+    for n in seqs:
+        ds = [e0.elapsed_time(e1) for m, e0, e1 in launch_events if m == n]
+        f = flops(data[n][0], HEADS, n, DIM, a.causal, "fwd")
+        cfg = _lib.config_desc(_lib.K_FWD, DIM, _lib.F16, _lib.pick_config(_lib.K_FWD, DIM, _lib.F16, a.causal, n))
+        tf = f / (sum(ds) / len(ds) * 1e-3) / 1e12
+        per_n.append({"seq": n, "batch": data[n][0], "entry": f"{cfg['waves']} waves x {cfg['tiles']} tiles "
+                      f"({cfg['block_m']} query rows per workgroup)", "avg_launch_us": round(1e3 * sum(ds) / len(ds), 2),
+                      "tflops": round(tf, 1), "frac": round(tf / PEAK_F16_TFLOPS, 4)})
     roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                 "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic,
                 "kernel": f"tattn::fwd_pipe_kernel (fp16, D=64, {'causal' if a.causal else 'non-causal'})",
                 "avg_launch_ms": kernel_ms, "launches": len(durations),
-                "flops_per_launch": fwd_flops / len(durations)}
+                "flops_per_launch": fwd_flops / len(durations), "per_n": per_n}
 
     # ---- sweep: per N, forward and fwd+bwd, causal and non-causal -------------------------
     sweep = []
@@ -276,6 +351,14 @@ def main() -> int:
         "roofline": roofline,
         "sweep": sweep,
     }
+    if not a.no_accuracy and not a.no_sweep:
+        out["accuracy"] = accuracy(data)
+        out["accuracy_worst"] = {
+            "fwd_max_abs_err": max(r["max_abs_err"] for r in out["accuracy"] if r["what"] == "o"),
+            "fwd_mean_abs_err": max(r["mean_abs_err"] for r in out["accuracy"] if r["what"] == "o"),
+            "grad_max_abs_err": max(r["max_abs_err"] for r in out["accuracy"] if r["what"] != "o"),
+            "envelope": 2e-3,
+        }
     if not a.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

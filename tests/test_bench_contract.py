@@ -27,6 +27,21 @@ def test_recorded_traffic_is_read_from_the_profile():
     assert t is not None and algorithmic <= t < 1.01 * algorithmic
 
 
+def test_cpu_baseline_threads_follow_the_host_budget(monkeypatch):
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    import os
+
+    cores = len(os.sched_getaffinity(0))
+    monkeypatch.delenv("OMP_NUM_THREADS", raising=False)
+    assert bench.cpu_threads()[:2] == (cores, cores)
+    if cores > 1:
+        monkeypatch.setenv("OMP_NUM_THREADS", "1")
+        got = bench.cpu_threads()
+        assert got[:2] == (cores, 1) and "OMP_NUM_THREADS=1" in got[2]
+
+
 @pytest.mark.gpu
 def test_default_contract_on_one_gpu():
     """A short run of the headline step (no sweep) prints one JSON line with every required key."""
@@ -45,6 +60,9 @@ def test_default_contract_on_one_gpu():
     assert roof["bound"] == "mfma" and roof["unit"] == "TFLOP/s" and roof["peak"] == 2516.6
     assert abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-9 and 0 < roof["frac"] < 1
     assert roof["traffic"] is not None and roof["launches"] == 2 * 6
+    assert [r["seq"] for r in roof["per_n"]] == [512, 1024, 2048, 4096, 8192, 16384]
+    assert all(0 < r["frac"] < 1 and r["avg_launch_us"] > 0 for r in roof["per_n"])
     cpu = out["cpu_baseline"]
     assert cpu["kind"] == "port" and cpu["cores"] >= 1 and cpu["value"] > 0 and cpu["sample"]
+    assert cpu["threads"] == cpu["cores"] <= cpu["affinity_cores"] and cpu["thread_choice"]
     assert 0 < out["value"] < 2516.6

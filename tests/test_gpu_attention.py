@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from helpers import emulated_backward as _emulated_backward
-from helpers import golden, rand
+from helpers import flip_cap, golden, max_err, rand
 from oracle import exact
 from oracle.reference import LOG2E, naive_attention
 
@@ -159,9 +159,11 @@ def test_any_softmax_scale(dtype, scale):
             for name, g_, w in zip(("dq", "dk", "dv"), got, (qr.grad, kr.grad, vr.grad)):
                 torch.testing.assert_close(g_, w, **t32, msg=lambda msg: f"{name} causal={causal}: {msg}")
         else:
+            _print_autograd_error(f"scale={scale} {dtype} causal={causal}", q, k, v, do, got, causal, scale)
             want, flips = _emulated_backward(q, k, v, o, m, do, causal, scale)
+            cap = flip_cap(dtype, scale)
             for name, g_, w, bnd in zip(("dq", "dk", "dv"), got, want, flips):
-                excess = ((g_.float() - w).abs() - t["atol"] - t["rtol"] * w.abs() - bnd).max().item()
+                excess = ((g_.float() - w).abs() - t["atol"] - t["rtol"] * w.abs() - bnd.clamp(max=cap)).max().item()
                 assert excess <= 0, f"{name} causal={causal}: error exceeds the bound by {excess:.3e}"
 
 
@@ -521,6 +523,16 @@ def test_inference_path_matches_autograd_path(causal, dtype):
     assert m2 is None and m3 is not None and torch.equal(o2, o3)
 
 
+def _print_autograd_error(tag, q, k, v, do, got, causal, scale):
+    """Prints the gradients' max abs error against float32 autograd (the yardstick these
+    ill-conditioned rows are not held to; recorded for comparison)."""
+    qr, kr, vr = (x.detach().float().clone().requires_grad_() for x in (q, k, v))
+    naive_attention(qr, kr, vr, causal=causal, sm_scale=scale).backward(do.float())
+    errs = ", ".join(f"{nm} {max_err(g_, w):.3e}" for nm, g_, w in zip(("dq", "dk", "dv"), got,
+                                                                        (qr.grad, kr.grad, vr.grad)))
+    print(f"{tag}: max abs err vs float32 autograd: {errs}", flush=True)
+
+
 def _stress_inputs(kind, dtype, n, d=64):
     g = torch.Generator().manual_seed(123 + n)
     q, k, v, do = (torch.randn(1, 2, n, d, generator=g) for _ in range(4))
@@ -566,7 +578,39 @@ def test_softmax_stress_matches_definition(kind, n, causal, dtype):
         sf = sf.masked_fill(torch.ones(n, n, device=DEV, dtype=torch.bool).triu(1), float("-inf"))
     torch.testing.assert_close(m, torch.logsumexp(sf, -1) * LOG2E, atol=8e-3, rtol=1e-4)
     got = _backward(q, k, v, o, m, do, causal, scale)
+    _print_autograd_error(f"stress {kind} n={n} {dtype} causal={causal}", q, k, v, do, got, causal, scale)
     want, flips = _emulated_backward(q, k, v, o, m, do, causal, scale)
+    cap = flip_cap(dtype, scale)
     for name, g_, w, bnd in zip(("dq", "dk", "dv"), got, want, flips):
-        excess = ((g_.float() - w).abs() - t["atol"] - t["rtol"] * w.abs() - bnd).max().item()
+        excess = ((g_.float() - w).abs() - t["atol"] - t["rtol"] * w.abs() - bnd.clamp(max=cap)).max().item()
         assert excess <= 0, f"{name}: error exceeds the bound by {excess:.3e}"
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_nan_in_one_query_row_stays_in_its_rows(dtype, causal):
+    """A NaN in query row r: as in the reference (NaN scores propagate through exp2 and the
+    sums, masked scores are replaced, not multiplied), output row r and its M are NaN and every
+    other row is finite; dq is NaN in row r only; dv is NaN exactly for the keys row r sees (all
+    keys, or keys <= r when causal), and so is dk for those keys. (Causal dk of keys past r is
+    left open: dS = P (dP - delta) gives 0 * NaN there wherever a block holds row r, in the
+    reference's kernels and in autograd alike, so that set depends on the blocking.)"""
+    from tattn.api import _backward, _forward
+
+    n, row = 150, 77
+    q, k, v, do = (r((1, 2, n, 64), dtype, 1300 + s) for s in range(4))
+    q[0, 1, row, 5] = float("nan")
+    o, m = _forward(q, k, v, causal, 0.125)
+    bad_rows = torch.zeros(n, dtype=torch.bool, device=DEV)
+    bad_rows[row] = True
+    assert torch.isnan(o[0, 1]).all(-1).eq(bad_rows).all() and torch.isfinite(o[0, 1][~bad_rows]).all()
+    assert torch.isfinite(o[0, 0]).all() and torch.isfinite(m[0, 0]).all()
+    assert torch.isnan(m[0, 1, row]) and torch.isfinite(m[0, 1][~bad_rows]).all()
+    dq, dk, dv = _backward(q, k, v, o, m, do, causal, 0.125)
+    assert torch.isfinite(dq[0, 0]).all() and torch.isfinite(dk[0, 0]).all() and torch.isfinite(dv[0, 0]).all()
+    assert torch.isnan(dq[0, 1]).any(-1).eq(bad_rows).all()
+    seen = torch.arange(n, device=DEV) <= row if causal else torch.ones(n, dtype=torch.bool, device=DEV)
+    assert torch.isnan(dv[0, 1]).any(-1).eq(seen).all() and torch.isfinite(dv[0, 1][~seen]).all()
+    assert torch.isnan(dk[0, 1][seen]).any(-1).all()
+    if not causal:
+        assert torch.isnan(dk[0, 1]).any(-1).all()

@@ -16,7 +16,14 @@ materialised attention and its autograd on the same seeded inputs.
 - The reference bench's accuracy recipe at every length, held to the errors the reference
   published for its own kernels (tests/golden/t4_accuracy.json).
 
-Tolerances: fp16 |err| <= 2e-3 + 2e-3 |ref| (output and gradients), fp32 1e-5 + 1e-5 |ref|.
+- Config 1 of the benchmark plan: fp32 [2, 4, 128, 64], non-causal, forward + backward, against
+  float32 materialised attention and against the oracle's tiled algorithm (16 x 16 blocks).
+
+Bounds: the envelope as flat maxima (max abs error <= 2e-3 in fp16 for outputs and gradients,
+<= 1e-5 in fp32; measured maxima are printed), plus the per-element envelope
+|err| <= 2e-3 + 2e-3 |ref| (fp32 1e-5 + 1e-5 |ref|). fp16 gradients of causal attention take the
+flat cap F16_CAUSAL_GRAD_MAX = 4e-3 instead (tests/helpers.py gives the mechanism and the measured
+error of the reference algorithm itself on these inputs).
 The float32 reference is computed a few heads at a time so its N x N matrices stay near 1 GiB."""
 
 import math
@@ -24,8 +31,8 @@ import math
 import pytest
 import torch
 
-from helpers import emulated_backward, rand
-from oracle.reference import naive_attention
+from helpers import F16_CAUSAL_GRAD_MAX, F16_MAX, F32_MAX, check_max, emulated_backward, flip_cap, rand
+from oracle.reference import naive_attention, tiled_backward, tiled_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -60,6 +67,18 @@ def _reference(q, k, v, do, causal):
     return outs
 
 
+def _check_all(tag, got, want, dtype, causal):
+    """Flat maxima and the per-element envelope for o, dq, dk, dv."""
+    tol = F16_TOL if dtype == torch.float16 else F32_TOL
+    for name, g, w in zip(("o", "dq", "dk", "dv"), got, want):
+        if dtype == torch.float16:
+            bound = F16_CAUSAL_GRAD_MAX if (causal and name != "o") else F16_MAX
+        else:
+            bound = F32_MAX
+        check_max(f"{tag} {name}", g, w, bound)
+        torch.testing.assert_close(g, w, **tol, msg=lambda m: f"{name} {tag}: {m}")
+
+
 def _run(q, k, v, do, causal):
     from tattn import attention
 
@@ -79,9 +98,7 @@ def test_edge_shapes_noncontiguous(d, n, causal, dtype):
     assert not q.is_contiguous() or n == 1
     got = _run(q, k, v, do, causal)
     want = _reference(q, k, v, do, causal)
-    tol = F16_TOL if dtype == torch.float16 else F32_TOL
-    for name, g, w in zip(("o", "dq", "dk", "dv"), got, want):
-        torch.testing.assert_close(g, w, **tol, msg=lambda m: f"{name} d={d} n={n} causal={causal}: {m}")
+    _check_all(f"edge {dtype} d={d} n={n} causal={causal}", got, want, dtype, causal)
 
 
 @pytest.mark.parametrize("n", [512, 1024, 2048, 4096, 8192, 16384])
@@ -92,8 +109,7 @@ def test_full_size_fp16(n, causal):
     q, k, v, do = (torch.randn(b, 16, n, 64, device=DEV, dtype=torch.float16, generator=g) for _ in range(4))
     got = _run(q, k, v, do, causal)
     want = _reference(q, k, v, do, causal)
-    for name, gt, w in zip(("o", "dq", "dk", "dv"), got, want):
-        torch.testing.assert_close(gt, w, **F16_TOL, msg=lambda m: f"{name} n={n} causal={causal}: {m}")
+    _check_all(f"full n={n} causal={causal}", got, want, torch.float16, causal)
 
 
 @pytest.mark.parametrize("d,dtype", [(128, torch.float16), (64, torch.bfloat16), (128, torch.bfloat16)])
@@ -120,7 +136,9 @@ def test_long_context_scaled_inputs_and_memory(causal):
                    for _ in range(4))
     got = _run(q, k, v, do, causal)
     want = _reference(q, k, v, do, causal)
+    # 0.5-scaled inputs: every gradient stays inside the flat fp16 envelope, causal included.
     for name, gt, w in zip(("o", "dq", "dk", "dv"), got, want):
+        check_max(f"long causal={causal} {name}", gt, w, F16_MAX)
         torch.testing.assert_close(gt, w, **F16_TOL, msg=lambda m: f"{name} causal={causal}: {m}")
     del got, want
 
@@ -141,21 +159,29 @@ def test_long_context_scaled_inputs_and_memory(causal):
 @pytest.mark.parametrize("causal", [False, True])
 def test_many_heads_short_rows(causal):
     """65,536 (batch, head) pairs of 24 tokens each (B=1024, H=64, D=16): the largest head count
-    here. Output against float32 attention; gradients against the backward with the reference
-    kernels' rounding points (causal rows 0 and 1 see one or two keys, where dP - delta cancels
-    and the rounding of the stored O dominates, so float32 autograd is not the yardstick)."""
+    here. Output against float32 attention (flat 2e-3). Gradients against float32 autograd under
+    the flat causal cap (measured 3.7e-3 causal, 2.3e-3 not; the reference's rounding points
+    computed exactly give 3.5e-3 and 3.4e-3 on the same inputs: rows of one or two keys make
+    dP - delta cancel, so the rounding of the stored O and of dS dominates), and against the
+    backward with those rounding points within the envelope plus the capped flip allowance."""
     from tattn.api import _backward, _forward
 
     g = torch.Generator(device=DEV).manual_seed(24 + int(causal))
     q, k, v, do = (torch.randn(1024, 64, 24, 16, device=DEV, dtype=torch.float16, generator=g) for _ in range(4))
     scale = 0.25
     o, m = _forward(q, k, v, causal, scale)
-    ref = naive_attention(q.float(), k.float(), v.float(), causal=causal, sm_scale=scale)
-    torch.testing.assert_close(o.float(), ref, **F16_TOL)
+    qr, kr, vr = (t.float().requires_grad_() for t in (q, k, v))
+    ref = naive_attention(qr, kr, vr, causal=causal, sm_scale=scale)
+    ref.backward(do.float())
+    check_max(f"many heads causal={causal} o", o, ref.detach(), F16_MAX)
+    torch.testing.assert_close(o.float(), ref.detach(), **F16_TOL)
     got = _backward(q, k, v, o, m, do, causal, scale)
+    for name, g_, w in zip(("dq", "dk", "dv"), got, (qr.grad, kr.grad, vr.grad)):
+        check_max(f"many heads causal={causal} {name} vs float32 autograd", g_, w, F16_CAUSAL_GRAD_MAX)
     want, flips = emulated_backward(q, k, v, o, m, do, causal, scale)
+    cap = flip_cap(q.dtype, scale)
     for name, g_, w, bnd in zip(("dq", "dk", "dv"), got, want, flips):
-        excess = ((g_.float() - w).abs() - F16_TOL["atol"] - F16_TOL["rtol"] * w.abs() - bnd).max().item()
+        excess = ((g_.float() - w).abs() - F16_TOL["atol"] - F16_TOL["rtol"] * w.abs() - bnd.clamp(max=cap)).max().item()
         assert excess <= 0, f"{name} causal={causal}: error exceeds the bound by {excess:.3e}"
 
 
@@ -270,6 +296,8 @@ def test_forward_error_no_worse_than_published(e):
     if n > 4096:
         q, k, v = (t[:1, :2].contiguous() for t in (q, k, v))
     err = (attention(q, k, v, causal=causal).float() - _forward_reference(q, k, v, causal)).abs()
+    print(f"recipe fwd n={n} causal={causal}: max {err.max().item():.3e} mean {err.mean().item():.3e}")
+    assert err.max().item() <= F16_MAX, err.max().item()
     assert err.mean().item() <= 1.25 * e["mean_abs_err"], (err.mean().item(), e["mean_abs_err"])
     assert err.max().item() <= 2.5 * e["max_abs_err"], (err.max().item(), e["max_abs_err"])
 
@@ -290,5 +318,29 @@ def test_gradient_error_no_worse_than_published(n, causal):
     naive_attention(qr, kr, vr, causal=causal).backward(do.float())
     for label, got, want in (("dq", qg.grad, qr.grad), ("dk", kg.grad, kr.grad), ("dv", vg.grad, vr.grad)):
         pub = next(e for e in PUBLISHED if e.get("grad") == label and e["seq"] == n and e["causal"] == causal)
-        err = (got.float() - want).abs().max().item()
+        err = check_max(f"recipe grad n={n} causal={causal} {label}", got, want, F16_MAX)
         assert err <= 2.0 * pub["max_abs_err"], (label, err, pub["max_abs_err"])
+
+
+def test_config1_fp32_forward_backward():
+    """Config 1 of the benchmark plan (the reference's CPU-runnable case): fp32 q, k, v
+    [2, 4, 128, 64] N(0,1) from a seed, non-causal, dO ~ N(0,1). Output, M and dq/dk/dv against
+    float32 materialised attention and its autograd, and against the oracle's tiled forward and
+    backward with the reference's default 16 x 16 blocks (reference.py:29-102): flat 1e-5."""
+    from tattn.api import _backward, _forward
+
+    q, k, v, do = (rand((2, 4, 128, 64), torch.float32, 31 + i, DEV) for i in range(4))
+    scale = 1.0 / math.sqrt(64)
+    o, m = _forward(q, k, v, False, scale)
+    dq, dk, dv = _backward(q, k, v, o, m, do, False, scale)
+    qr, kr, vr = (t.clone().requires_grad_() for t in (q, k, v))
+    ref = naive_attention(qr, kr, vr, causal=False)
+    ref.backward(do)
+    for name, got, want in zip(("o", "dq", "dk", "dv"), (o, dq, dk, dv), (ref.detach(), qr.grad, kr.grad, vr.grad)):
+        check_max(f"config1 {name} vs float32 autograd", got, want, F32_MAX)
+    qc, kc, vc, dc = (t.cpu() for t in (q, k, v, do))
+    o_t, m_t = tiled_forward(qc, kc, vc, False, scale)
+    check_max("config1 o vs tiled", o.cpu(), o_t, F32_MAX)
+    check_max("config1 M vs tiled", m.cpu(), m_t, F32_MAX)
+    for name, got, want in zip(("dq", "dk", "dv"), (dq, dk, dv), tiled_backward(qc, kc, vc, o_t, m_t, dc, False, scale)):
+        check_max(f"config1 {name} vs tiled", got.cpu(), want, F32_MAX)

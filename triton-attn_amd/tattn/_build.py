@@ -39,7 +39,6 @@ COMMON_FLAGS = [
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
-    "-fno-honor-nans",
 ]
 
 

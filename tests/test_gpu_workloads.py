@@ -344,3 +344,23 @@ def test_config1_fp32_forward_backward():
     check_max("config1 M vs tiled", m.cpu(), m_t, F32_MAX)
     for name, got, want in zip(("dq", "dk", "dv"), (dq, dk, dv), tiled_backward(qc, kc, vc, o_t, m_t, dc, False, scale)):
         check_max(f"config1 {name} vs tiled", got.cpu(), want, F32_MAX)
+
+
+def test_comparison_suite_runs_one_short_length(tmp_path):
+    """tattn.benchsuite end to end on the GPU at one short length (N=256, 1,024 tokens): every
+    cell present with a status, tattn's cells timed, errors measured, and the report's schema
+    check and renderer accept the file."""
+    import json
+
+    from tattn import benchsuite, report
+
+    res = benchsuite.run([256], tokens=1024, heads=4, dim=64)
+    assert len(res["cells"]) == 5 * 2 * 2
+    mine = [c for c in res["cells"] if c["impl"] == "tattn"]
+    assert all(c["status"] == "ok" and c["ms"] > 0 and c["tflops"] > 0 for c in mine)
+    errs = [e for e in res["errors"] if e["impl"] == "tattn" and e["tensor"] == "o"]
+    assert len(errs) == 2 and all(e["max_abs"] <= F16_MAX for e in errs)
+    path = tmp_path / "suite.json"
+    path.write_text(json.dumps(res))
+    assert report.main([str(path), "--check"]) == 0
+    assert "## Forward, TFLOP/s" in report.render(res)

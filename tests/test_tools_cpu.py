@@ -1,5 +1,9 @@
 """CPU tests of the measurement tools: the ISA parser of tattn.diagnose (on a hand-written
-assembly listing and on the compiled forward kernel), and the markdown report of tattn.report."""
+assembly listing and on the compiled forward kernel), the comparison suite's cell and error
+assembly (tattn.benchsuite, with fake implementations and a fixed timer on the CPU), and the
+markdown report of tattn.report."""
+
+import json
 
 import pytest
 
@@ -107,38 +111,99 @@ def test_forward_pipeline_main_loop_isa(fwd_asm):
     assert ml["scratch"] == 0 and ml["wait_vmcnt0"] == 0
 
 
-def _fake_result():
-    rows = []
-    for impl, f in (("tattn", 900.0), ("sdpa_flash", 400.0), ("naive", 50.0)):
-        for mode in ("fwd", "fwd+bwd"):
-            for causal in (False, True):
-                for seq, batch in ((1024, 16), (16384, 1)):
-                    rows.append({"impl": impl, "seq": seq, "batch": batch, "causal": causal, "mode": mode,
-                                 "ms": 1.0, "tflops": f * (0.5 if mode == "fwd+bwd" else 1.0),
-                                 "peak_extra_mib": 100.0})
-    rows.append({"impl": "sdpa_math", "seq": 16384, "batch": 1, "causal": False, "mode": "fwd", "oom": True})
-    return {
-        "env": {"gpu": "AMD Instinct MI355X", "arch": "gfx950:sramecc+:xnack-", "memory_gib": 288,
-                "torch": "2.10", "hip": "7.0", "python": "3.10"},
-        "config": {"dim": 64, "heads": 16, "tokens": 16384, "timer": "median", "flops": "4 n^2 d", "data": "randn"},
-        "rows": rows,
-        "accuracy": [{"impl": "tattn", "seq": 1024, "causal": False, "max_abs_err": 1e-3, "mean_abs_err": 1e-5},
-                     {"impl": "tattn", "seq": 1024, "causal": False, "grad": "dq", "max_abs_err": 2e-3}],
-        "table_picks": {"16384": {"fwd": 3, "bwd_dkdv": 1, "bwd_dq": 1}},
-        "fp16_matmul_4096_tflops": 1500.0,
-    }
+def _suite_result():
+    """A small tattn-suite/1 result built by the suite's own sweep and error code on the CPU, with
+    fake implementations and a fixed timer."""
+    import torch
+
+    from tattn import benchsuite as bs
+
+    def scaled(f):
+        return lambda q, k, v, causal: bs.materialised(q, k, v, causal) * f
+
+    def broken(q, k, v, causal):
+        raise RuntimeError("No available kernel. Aborting execution.\nmore text")
+
+    impls = [bs.Impl("tattn", "tattn", scaled(1.0)), bs.Impl("sdpa_flash", "flash", broken),
+             bs.Impl("materialised", "materialised", bs.materialised)]
+    inputs = {n: bs.make_inputs(n, 64, 2, 16, "cpu", torch.float32) for n in (16, 32)}
+    times = {"tattn": 1.0, "materialised": 4.0}
+
+    def timer(call, reset):
+        call()
+        reset()
+        return times[current[0]], 3.0
+
+    current = ["tattn"]
+    orig = bs.call_for
+
+    def call_for(impl, x, causal, passes):
+        current[0] = impl.name
+        return orig(impl, x, causal, passes)
+
+    bs.call_for = call_for
+    try:
+        cells = bs.sweep_cells(impls, inputs, heads=2, dim=16, timer=timer)
+    finally:
+        bs.call_for = orig
+    errors = bs.measure_errors(impls, inputs, grad_seqs=(32,))
+    return {"schema": "tattn-suite/1",
+            "device": {"name": "AMD Instinct MI355X", "arch": "gfx950:sramecc+:xnack-", "memory_gib": 288,
+                       "torch": "2.10", "hip": "7.0", "python": "3.10"},
+            "method": {"tokens": 64, "heads": 2, "dim": 16, "dtype": "float32", "timer": "fixed",
+                       "flops": "4 n^2 d", "data": "randn"},
+            "cells": cells, "errors": errors, "gemm_tflops": 1500.0,
+            "picks": {"16/none": {"fwd": 1, "bwd_dkdv": 0, "bwd_dq": 0}}, "autotuned": None}
+
+
+def test_suite_sweep_assembles_every_cell():
+    from tattn import benchsuite as bs
+
+    res = _suite_result()
+    cells = res["cells"]
+    assert len(cells) == 3 * 2 * 2 * 2  # impls x N x masks x passes
+    ok = [c for c in cells if c["impl"] == "tattn"]
+    assert all(c["status"] == "ok" and c["ms"] == 1.0 and c["peak_mib"] == 3.0 for c in ok)
+    c = next(c for c in ok if c["n"] == 32 and c["mask"] == "causal" and c["pass"] == "fwd+bwd")
+    assert c["b"] == 2 and c["tflops"] == bs.counted_flops(2, 2, 32, 16, True, "fwd+bwd") / 1e-3 / 1e12
+    bad = [c for c in cells if c["impl"] == "sdpa_flash"]
+    assert all(c["status"] == "unsupported" and c["note"] == "No available kernel. Aborting execution."
+               for c in bad)
+
+
+def test_suite_errors_cover_outputs_and_gradients():
+    errs = _suite_result()["errors"]
+    fwd = {(e["impl"], e["n"], e["mask"]) for e in errs if e["tensor"] == "o"}
+    assert fwd == {(i, n, m) for i in ("tattn", "materialised") for n in (16, 32) for m in ("none", "causal")}
+    assert all(e["max_abs"] < 1e-5 for e in errs)  # float32 inputs: same math as the reference
+    grads = [(e["n"], e["mask"], e["tensor"]) for e in errs if e["tensor"] != "o"]
+    assert sorted(grads) == sorted((32, m, t) for m in ("none", "causal") for t in ("dq", "dk", "dv"))
 
 
 def test_report_renders_every_section():
-    text = report.render(_fake_result())
-    assert "Best tattn forward: 900.0 TFLOP/s (35.8% of" in text
-    for title in ("Forward, non-causal", "Forward, causal", "Forward + backward, non-causal",
-                  "Forward + backward, causal", "Peak extra memory", "Accuracy", "Table picks"):
+    res = _suite_result()
+    assert report.problems(res) == []
+    text = report.render(res)
+    for title in ("Forward, TFLOP/s", "Forward + backward, TFLOP/s", "Peak memory", "Accuracy",
+                  "Cells that did not run", "Tile-table entries used"):
         assert f"## {title}" in text
-    # tattn over SDPA flash: 900/400 in every cell, both modes.
-    assert "| SDPA flash | 2.25–2.25× | 2.25–2.25× |" in text
-    assert "OOM" in text and "| 16,384 (1) |" in text
-    assert "16384: 3/1/1" in text
+    assert "| tattn ÷ fastest other |" in text and "| 4.00× |" in text  # 1 ms against 4 ms
+    assert "SDPA flash, unsupported: 16/none/fwd (No available kernel. Aborting execution.)" in text
+    assert "16/none: 1/0/0" in text
+
+
+def test_report_check_flags_broken_files(tmp_path):
+    res = _suite_result()
+    good = tmp_path / "good.json"
+    good.write_text(json.dumps(res))
+    assert report.main([str(good), "--check"]) == 0
+    res["cells"][0].pop("status")
+    res["errors"][0]["max_abs"] = float("nan")
+    bad = tmp_path / "bad.json"
+    bad.write_text(json.dumps(res))
+    assert report.main([str(bad), "--check"]) == 1
+    assert any("lacks ['status']" in p for p in report.problems(res))
+    assert any("non-finite" in p for p in report.problems(res))
 
 
 @pytest.fixture(scope="module")

@@ -42,7 +42,10 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I = ctypes.c_int
 _F = ctypes.c_float
-_STR4 = ctypes.POINTER(ctypes.c_int64)
+# Stride arguments (const int64_t[4]) are bound as plain addresses: callers pass a ctypes int64
+# array, or the address of four consecutive int64 values inside a larger one (one array per call
+# holds every tensor's strides).
+_STR4 = ctypes.c_void_p
 
 _SIGS = {
     "tattn_abi_version": (_I, []),
@@ -103,6 +106,24 @@ def check(rc: int, what: str) -> None:
 
 def strides4(t: torch.Tensor):
     return (ctypes.c_int64 * 4)(*t.stride())
+
+
+_stride_blocks: dict[tuple, tuple] = {}
+
+
+def stride_block(*ts: torch.Tensor):
+    """One int64 array with the four strides of each tensor, and the address of each tensor's
+    four. Arrays are kept per distinct stride tuple (read-only for the library), so repeated
+    calls on the same layouts build none."""
+    key = tuple(t.stride() for t in ts)
+    hit = _stride_blocks.get(key)
+    if hit is None:
+        if len(_stride_blocks) > 1024:
+            _stride_blocks.clear()
+        arr = (ctypes.c_int64 * (4 * len(ts)))(*(s for st in key for s in st))
+        base = ctypes.addressof(arr)
+        hit = _stride_blocks[key] = (arr, [base + 32 * i for i in range(len(ts))])
+    return hit
 
 
 def num_configs(kernel: int, d: int, dtype: int) -> int:

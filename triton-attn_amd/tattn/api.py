@@ -11,6 +11,7 @@ raises instead of computing.
 
 from __future__ import annotations
 
+import contextlib
 import math
 import os
 from typing import Any, Callable, Union
@@ -67,8 +68,17 @@ def _bucket(n: int) -> int:
     return 1 << max(0, (n - 1).bit_length())
 
 
+_device_ok: dict[int, bool] = {}  # device index -> hip_available (fixed for the process)
+
+
 def _require_gpu(t: torch.Tensor) -> None:
-    if not hip_available(t.device):
+    idx = t.get_device()
+    if _device_ok.get(idx):
+        return
+    ok = hip_available(t.device)
+    if idx >= 0:
+        _device_ok[idx] = ok
+    if not ok:
         if t.device.type != "cuda":
             raise RuntimeError(
                 f"tattn runs on a ROCm gfx950 (MI355X) GPU; got tensors on {t.device}"
@@ -80,6 +90,8 @@ def _require_gpu(t: torch.Tensor) -> None:
 def _kernel_layout(t: torch.Tensor) -> torch.Tensor:
     """The kernels read rows with 16-byte vector loads: unit d stride, 16-byte aligned rows and
     base. Anything else is copied to a contiguous tensor (same values)."""
+    if t.is_contiguous() and t.data_ptr() % 16 == 0:  # rows of 16+ elements: 16-byte multiples
+        return t
     vec = 16 // t.element_size()
     ok = (
         t.stride(-1) == 1
@@ -109,8 +121,21 @@ def _resolve(kernel: int, d: int, dtype: torch.dtype, config: Config, causal: bo
     return hits[0]
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_current_device = getattr(torch._C, "_cuda_getDevice", torch.cuda.current_device)
+
+
 def _stream(t: torch.Tensor) -> int:
+    """Handle of the current stream of t's device (the stream torch enqueues on)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _on_device(t: torch.Tensor):
+    """Device guard for the library call: a no-op when t's device is already current."""
+    idx = t.get_device()
+    return contextlib.nullcontext() if idx == _current_device() else torch.cuda.device(idx)
 
 
 # Optional first-use timing of the tile table. The reference autotunes on the first call of each
@@ -175,20 +200,21 @@ def _forward(
     save_lse=False (no backward will follow) skips M: neither allocated nor stored, M is None."""
     _require_gpu(q)
     lib = _lib.load()
-    q, k, v = (_kernel_layout(t) for t in (q, k, v))
+    q, k, v = _kernel_layout(q), _kernel_layout(k), _kernel_layout(v)
     z, h, n, d = q.shape
     o = torch.empty_like(q)
-    m = torch.empty((z, h, n), device=q.device, dtype=torch.float32) if save_lse else None
-    cid = _resolve(_lib.K_FWD, d, q.dtype, config, causal, n)
+    m = q.new_empty((z, h, n), dtype=torch.float32) if save_lse else None
+    cid = -1 if config is None else _resolve(_lib.K_FWD, d, q.dtype, config, causal, n)
     if q.numel() == 0:  # no rows: nothing to launch (the reference's empty grid launches nothing)
         return o, m
+    _, (sq, sk, sv, so) = _lib.stride_block(q, k, v, o)
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), m.data_ptr() if m is not None else None,
-            _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(o),
-            z, h, n, d, _DTYPES[q.dtype], int(causal), float(scale))
-    with torch.cuda.device(q.device):
-        if config is None:
-            cid = _tuned_id(_lib.K_FWD, q, d, causal, n, lambda c: lib.tattn_fwd(*args, c, _stream(q)))
-        rc = lib.tattn_fwd(*args, cid, _stream(q))
+            sq, sk, sv, so, z, h, n, d, _DTYPES[q.dtype], int(causal), float(scale))
+    with _on_device(q):
+        stream = _stream(q)
+        if config is None and _autotune:
+            cid = _tuned_id(_lib.K_FWD, q, d, causal, n, lambda c: lib.tattn_fwd(*args, c, stream))
+        rc = lib.tattn_fwd(*args, cid, stream)
     _lib.check(rc, "tattn_fwd")
     return o, m
 
@@ -202,11 +228,23 @@ def _backward(
     _require_gpu(q)
     lib = _lib.load()
     z, h, n, d = q.shape
-    q, k, v, do, o = (t.contiguous() for t in (q, k, v, do.to(q.dtype), o))
+    if do.dtype != q.dtype:
+        do = do.to(q.dtype)
+    q, k, v, do, o = q.contiguous(), k.contiguous(), v.contiguous(), do.contiguous(), o.contiguous()
     m = m.contiguous()
-    delta = torch.empty((z, h, n), device=q.device, dtype=torch.float32)
+    delta = q.new_empty((z, h, n), dtype=torch.float32)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     if q.numel() == 0:
+        return dq, dk, dv
+    code = _DTYPES[q.dtype]
+    _, (st,) = _lib.stride_block(q)
+    if config is None and not _autotune:
+        # The whole backward in one library call: preprocess, dK/dV, dQ in stream order.
+        with _on_device(q):
+            rc = lib.tattn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+                               dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), m.data_ptr(), delta.data_ptr(), st,
+                               z, h, n, d, code, int(causal), float(scale), -1, _stream(q))
+        _lib.check(rc, "tattn_bwd")
         return dq, dk, dv
     if isinstance(config, dict) and ("dkdv" in config or "dq" in config):
         kid = _resolve(_lib.K_BWD_DKDV, d, q.dtype, config.get("dkdv"), causal, n)
@@ -214,14 +252,12 @@ def _backward(
     else:
         kid = _resolve(_lib.K_BWD_DKDV, d, q.dtype, config, causal, n)
         qid = _resolve(_lib.K_BWD_DQ, d, q.dtype, config, causal, n)
-    st = _lib.strides4(q)
-    code = _DTYPES[q.dtype]
-    stream = _stream(q)
     dkdv_args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                  m.data_ptr(), delta.data_ptr(), st, z, h, n, d, code, int(causal), float(scale))
     dq_args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), dq.data_ptr(), m.data_ptr(),
                delta.data_ptr(), st, z, h, n, d, code, int(causal), float(scale))
-    with torch.cuda.device(q.device):
+    with _on_device(q):
+        stream = _stream(q)
         _lib.check(lib.tattn_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta.data_ptr(), st,
                                             z, h, n, d, code, stream), "tattn_bwd_preprocess")
         if config is None:

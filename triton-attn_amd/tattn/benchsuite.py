@@ -1,218 +1,279 @@
-"""Comparison benchmark: tattn against PyTorch's attention backends on this GPU.
+"""Comparison suite: tattn against PyTorch's attention backends on the same GPU.
 
-The counterpart of the reference's benchmark (bench/bench.py:1-206): for every sequence length
-(batch x seq held at a fixed token count), causal and not, forward and forward+backward, it
-times
+Serves the purpose of the reference's benchmark script (bench/bench.py of
+amaanmithani/triton-attn): speed, memory and accuracy of the fused kernels next to the stock
+implementations, at a fixed token count per batch. Measurement semantics follow it where they
+must be comparable: the FLOP convention (4*B*H*N^2*D, halved when causal, fwd+bwd = 3.5x fwd),
+a cold-cache median timer (tattn.timing.do_bench) and peak memory above the inputs.
 
-  - tattn (this package's HIP kernels, table-picked tiles, or with --autotune the fastest
-    table entry timed on first use; the picks are recorded as the reference records its
-    autotune caches, bench/bench.py:176-201),
-  - torch SDPA with each backend (flash, memory-efficient, math), one at a time,
-  - naive materialised attention (the definition),
-
-with the reference's timer (tattn.timing.do_bench: cache flushed before each call, median over
-~100 ms after ~25 ms of warm-up) and records peak extra memory per call. It then measures the
-output error of every implementation against float32 materialised attention at every length
-(the float32 reference fits in HBM at 16k tokens here), tattn's gradient error against float32
-autograd at N = 1024 and 4096, and a plain fp16 4096^3 matmul as a GEMM-rate reference. Cells an
-implementation cannot run (unsupported backend, out of memory) are recorded, not fatal.
+The suite is a grid of cells: every implementation x sequence length x mask x pass (forward,
+forward+backward). Implementations are plain callables (q, k, v, causal) -> o; an
+implementation that cannot run a cell (backend missing for this GPU or dtype, out of memory) is
+recorded with its status, not fatal. Errors are measured separately on the same inputs: every
+implementation's forward output against float32 materialised attention, and tattn's gradients
+against float32 autograd at N = 1024 and 4096 (batch 0).
 
     python -m tattn.benchsuite [--seqs 512,...,16384] [--tokens 16384] [--heads 16] [--dim 64]
-                               [--autotune] [--out results/<gpu>.json]
+                               [--autotune] [--out results/<arch>.json]
 
-Render the result with `python -m tattn.report results/<gpu>.json`.
+Result schema "tattn-suite/1":
+    device   {name, arch, memory_gib, torch, hip, python}
+    method   {tokens, heads, dim, dtype, timer, flops, data}
+    cells    [{impl, n, b, mask: "none"|"causal", pass: "fwd"|"fwd+bwd", status: "ok"|"oom"|
+               "unsupported", ms, tflops, peak_mib, note}]
+    errors   [{impl, n, mask, tensor: "o"|"dq"|"dk"|"dv", max_abs, mean_abs}]
+    gemm_tflops, picks {n/mask: {kernel: table id}}, autotuned (or null)
+
+Render it with `python -m tattn.report FILE`.
 """
 
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import math
 import platform
 from pathlib import Path
-from typing import Any, Callable
+from typing import Any, Callable, Iterable
 
 import torch
-import torch.nn.functional as F
 
-from . import attention, autotune_cache, set_autotune
-from . import _lib
-from .timing import do_bench
-
-IMPLS = ("tattn", "sdpa_flash", "sdpa_efficient", "sdpa_math", "naive")
 REPO = Path(__file__).resolve().parents[2]
+PASSES = ("fwd", "fwd+bwd")
+MASKS = ("none", "causal")
 
 
-def flops(b: int, h: int, n: int, d: int, causal: bool, mode: str) -> float:
+def counted_flops(b: int, h: int, n: int, d: int, causal: bool, passes: str) -> float:
     """The reference's FLOP convention (bench/bench.py:31-35)."""
-    f = 4.0 * b * h * n * n * d
-    if causal:
-        f *= 0.5
-    return f * (3.5 if mode == "fwd+bwd" else 1.0)
+    per_fwd = 4.0 * b * h * n * n * d * (0.5 if causal else 1.0)
+    return per_fwd * (3.5 if passes == "fwd+bwd" else 1.0)
 
 
-def naive(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool) -> torch.Tensor:
-    """softmax(Q K^T / sqrt(D)) V, materialised, in the inputs' dtype (the comparator the
-    reference calls naive)."""
-    s = torch.matmul(q, k.transpose(-2, -1).contiguous()) * (1.0 / math.sqrt(q.shape[-1]))
+@dataclasses.dataclass(frozen=True)
+class Impl:
+    name: str
+    label: str
+    fn: Callable[[torch.Tensor, torch.Tensor, torch.Tensor, bool], torch.Tensor]
+
+
+def materialised(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool) -> torch.Tensor:
+    """softmax(Q K^T / sqrt(D)) V with the N x N matrix in memory; softmax in float32, products in
+    the inputs' dtype."""
+    s = torch.matmul(q, k.transpose(-2, -1).contiguous()) / math.sqrt(q.shape[-1])
     if causal:
         n = q.shape[-2]
         s = s.masked_fill(torch.ones(n, n, dtype=torch.bool, device=q.device).triu(1), float("-inf"))
     return torch.matmul(torch.softmax(s.float(), dim=-1).to(q.dtype), v)
 
 
-def _sdpa(backend) -> Callable[..., torch.Tensor]:
-    from torch.nn.attention import sdpa_kernel
+def default_impls() -> list[Impl]:
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
 
-    def run(q, k, v, causal):
-        with sdpa_kernel(backend):
-            return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+    from . import attention
 
-    return run
+    def backend(which):
+        def run(q, k, v, causal):
+            with sdpa_kernel(which):
+                return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+        return run
 
-
-def implementations() -> dict[str, Callable[..., torch.Tensor]]:
-    from torch.nn.attention import SDPBackend
-
-    return {
-        "tattn": lambda q, k, v, causal: attention(q, k, v, causal=causal),
-        "sdpa_flash": _sdpa(SDPBackend.FLASH_ATTENTION),
-        "sdpa_efficient": _sdpa(SDPBackend.EFFICIENT_ATTENTION),
-        "sdpa_math": _sdpa(SDPBackend.MATH),
-        "naive": naive,
-    }
-
-
-def measure(fn: Callable[[], Any], clear: Callable[[], None] = lambda: None) -> dict[str, Any]:
-    """Median ms and peak memory above the baseline of one call; `clear` drops state left by the
-    warm-up call (gradients) before the baseline is taken."""
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
-    try:
-        fn()
-        clear()
-        torch.cuda.synchronize()
-        torch.cuda.reset_peak_memory_stats()
-        base = torch.cuda.memory_allocated()
-        fn()
-        torch.cuda.synchronize()
-        peak = torch.cuda.max_memory_allocated() - base
-        return {"ms": do_bench(fn), "peak_extra_mib": peak / 2**20}
-    except torch.OutOfMemoryError:
-        torch.cuda.empty_cache()
-        return {"oom": True}
-    except RuntimeError as e:  # backend unavailable for this GPU, dtype or shape
-        torch.cuda.empty_cache()
-        return {"error": str(e).splitlines()[0][:200]}
+    return [
+        Impl("tattn", "tattn (HIP, gfx950)", lambda q, k, v, causal: attention(q, k, v, causal=causal)),
+        Impl("sdpa_flash", "SDPA flash", backend(SDPBackend.FLASH_ATTENTION)),
+        Impl("sdpa_efficient", "SDPA mem-efficient", backend(SDPBackend.EFFICIENT_ATTENTION)),
+        Impl("sdpa_math", "SDPA math", backend(SDPBackend.MATH)),
+        Impl("materialised", "materialised", materialised),
+    ]
 
 
-def run(seqs: list[int], tokens: int, heads: int, dim: int, autotune: bool = False) -> dict[str, Any]:
-    dev = torch.device("cuda")
-    _lib.load()
-    props = torch.cuda.get_device_properties(dev)
-    impls = implementations()
-    rows: list[dict[str, Any]] = []
-    accuracy: list[dict[str, Any]] = []
-    picks: dict[str, dict[str, int]] = {}
-    set_autotune(autotune)
-    for n in seqs:
-        b = max(1, tokens // n)
-        for causal in (False, True):
-            g = torch.Generator(device=dev).manual_seed(n)
-            q, k, v, do = (torch.randn(b, heads, n, dim, device=dev, dtype=torch.float16, generator=g)
-                           for _ in range(4))
-            for name, f in impls.items():
-                for mode in ("fwd", "fwd+bwd"):
-                    clear: Callable[[], None] = lambda: None  # noqa: E731
-                    if mode == "fwd":
-                        def fn(f=f, q=q, k=k, v=v, causal=causal) -> None:
-                            with torch.no_grad():
-                                f(q, k, v, causal)
-                    else:
-                        qg, kg, vg = (t.detach().clone().requires_grad_() for t in (q, k, v))
+@dataclasses.dataclass
+class Inputs:
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    do: torch.Tensor
 
-                        def fn(f=f, qg=qg, kg=kg, vg=vg, do=do, causal=causal) -> None:
-                            qg.grad = kg.grad = vg.grad = None
-                            f(qg, kg, vg, causal).backward(do)
+    @property
+    def b(self) -> int:
+        return self.q.shape[0]
 
-                        def clear(qg=qg, kg=kg, vg=vg) -> None:
-                            qg.grad = kg.grad = vg.grad = None
-                    r = measure(fn, clear)
-                    if "ms" in r:
-                        r["tflops"] = flops(b, heads, n, dim, causal, mode) / (r["ms"] * 1e-3) / 1e12
-                    rows.append({"impl": name, "seq": n, "batch": b, "causal": causal, "mode": mode, **r})
-                    print(json.dumps(rows[-1]), flush=True)
-            # Output error against float32 materialised attention (all heads, every length).
+
+def make_inputs(n: int, tokens: int, heads: int, dim: int, device, dtype=torch.float16) -> Inputs:
+    """N(0,1) values from a generator on `device` seeded with N (dO from the same stream)."""
+    g = torch.Generator(device=device).manual_seed(n)
+    shape = (max(1, tokens // n), heads, n, dim)
+    return Inputs(*(torch.randn(shape, device=device, dtype=dtype, generator=g) for _ in range(4)))
+
+
+def call_for(impl: Impl, x: Inputs, causal: bool, passes: str) -> tuple[Callable[[], None], Callable[[], None]]:
+    """(the call to time, a reset that drops what a previous call left behind)."""
+    if passes == "fwd":
+        def fwd() -> None:
             with torch.no_grad():
-                ref = naive(q.float(), k.float(), v.float(), causal)
-                for name, f in impls.items():
+                impl.fn(x.q, x.k, x.v, causal)
+        return fwd, lambda: None
+    leaves = [t.detach().clone().requires_grad_() for t in (x.q, x.k, x.v)]
+
+    def reset() -> None:
+        for t in leaves:
+            t.grad = None
+
+    def fwd_bwd() -> None:
+        reset()
+        impl.fn(*leaves, causal).backward(x.do)
+    return fwd_bwd, reset
+
+
+Timer = Callable[[Callable[[], None], Callable[[], None]], tuple[float, float]]
+
+
+def gpu_timer(call: Callable[[], None], reset: Callable[[], None]) -> tuple[float, float]:
+    """(median ms with a cold cache, MiB allocated at peak beyond what was live before the call)."""
+    from .timing import do_bench
+
+    call()
+    reset()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    live = torch.cuda.memory_allocated()
+    call()
+    torch.cuda.synchronize()
+    peak = (torch.cuda.max_memory_allocated() - live) / 2**20
+    return do_bench(call), peak
+
+
+def _status_of(exc: BaseException) -> tuple[str, str]:
+    if isinstance(exc, torch.OutOfMemoryError):
+        return "oom", "out of memory"
+    first = (str(exc).strip().splitlines() or [type(exc).__name__])[0]
+    return "unsupported", first[:160]
+
+
+def sweep_cells(impls: Iterable[Impl], inputs: dict[int, Inputs], heads: int, dim: int, timer: Timer,
+                after_cell: Callable[[], None] = lambda: None) -> list[dict[str, Any]]:
+    """Times every (implementation, N, mask, pass) cell; failures become a status, not an error."""
+    cells = []
+    for n, x in inputs.items():
+        for mask in MASKS:
+            causal = mask == "causal"
+            for impl in impls:
+                for passes in PASSES:
+                    cell: dict[str, Any] = {"impl": impl.name, "n": n, "b": x.b, "mask": mask, "pass": passes}
                     try:
-                        out = f(q, k, v, causal).float()
-                        accuracy.append({"impl": name, "seq": n, "causal": causal, "reference": "naive fp32",
-                                         "max_abs_err": (out - ref).abs().max().item(),
-                                         "mean_abs_err": (out - ref).abs().mean().item()})
-                        del out
-                    except (RuntimeError, torch.OutOfMemoryError) as e:
-                        accuracy.append({"impl": name, "seq": n, "causal": causal,
-                                         "error": str(e).splitlines()[0][:120]})
+                        call, reset = call_for(impl, x, causal, passes)
+                        ms, peak = timer(call, reset)
+                        cell.update(status="ok", ms=ms, peak_mib=peak,
+                                    tflops=counted_flops(x.b, heads, n, dim, causal, passes) / (ms * 1e-3) / 1e12)
+                    except (RuntimeError, torch.OutOfMemoryError) as exc:
+                        status, note = _status_of(exc)
+                        cell.update(status=status, note=note)
+                    after_cell()
+                    cells.append(cell)
+                    print(json.dumps(cell), flush=True)
+    return cells
+
+
+def measure_errors(impls: Iterable[Impl], inputs: dict[int, Inputs], grad_seqs=(1024, 4096)) -> list[dict[str, Any]]:
+    """Forward error of every implementation against float32 materialised attention (all heads),
+    and tattn's gradient error against float32 autograd on batch 0 at `grad_seqs`."""
+    out: list[dict[str, Any]] = []
+    impls = list(impls)
+    for n, x in inputs.items():
+        for mask in MASKS:
+            causal = mask == "causal"
+            with torch.no_grad():
+                ref = torch.cat([materialised(x.q[i:i + 1].float(), x.k[i:i + 1].float(), x.v[i:i + 1].float(), causal)
+                                 for i in range(x.b)])
+                for impl in impls:
+                    try:
+                        err = (impl.fn(x.q, x.k, x.v, causal).float() - ref).abs()
+                        out.append({"impl": impl.name, "n": n, "mask": mask, "tensor": "o",
+                                    "max_abs": err.max().item(), "mean_abs": err.mean().item()})
+                        del err
+                    except (RuntimeError, torch.OutOfMemoryError):
+                        pass
                 del ref
-            # tattn gradients against float32 autograd of the definition.
-            if n in (1024, 4096):
-                qs, ks, vs, dos = (t[:1].detach().clone() for t in (q, k, v, do))
-                qg, kg, vg = (t.clone().requires_grad_() for t in (qs, ks, vs))
-                attention(qg, kg, vg, causal=causal).backward(dos)
-                qr, kr, vr = (t.float().requires_grad_() for t in (qs, ks, vs))
-                naive(qr, kr, vr, causal).backward(dos.float())
-                for label, got, want in (("dq", qg.grad, qr.grad), ("dk", kg.grad, kr.grad),
-                                         ("dv", vg.grad, vr.grad)):
-                    accuracy.append({"impl": "tattn", "seq": n, "causal": causal, "grad": label,
-                                     "max_abs_err": (got.float() - want).abs().max().item()})
-            picks[f"{n}{'_causal' if causal else ''}"] = {
-                name: _lib.pick_config(kid, dim, _lib.F16, causal, n) for kid, name in _lib.KERNEL_NAMES.items()}
-            del q, k, v, do
-            torch.cuda.empty_cache()
-    a_ = torch.randn(4096, 4096, device=dev, dtype=torch.float16)
-    b_ = torch.randn(4096, 4096, device=dev, dtype=torch.float16)
-    mm_ms = do_bench(lambda: a_ @ b_)
+            tattn = next((i for i in impls if i.name == "tattn"), None)
+            if tattn is None or n not in grad_seqs:
+                continue
+            q, k, v, do = (t[:1].detach().clone() for t in (x.q, x.k, x.v, x.do))
+            got = [t.clone().requires_grad_() for t in (q, k, v)]
+            tattn.fn(*got, causal).backward(do)
+            want = [t.float().requires_grad_() for t in (q, k, v)]
+            materialised(*want, causal).backward(do.float())
+            for name, a, b in zip(("dq", "dk", "dv"), got, want):
+                e = (a.grad.float() - b.grad).abs()
+                out.append({"impl": "tattn", "n": n, "mask": mask, "tensor": name,
+                            "max_abs": e.max().item(), "mean_abs": e.mean().item()})
+    return out
+
+
+def device_info() -> dict[str, Any]:
+    p = torch.cuda.get_device_properties(0)
+    return {"name": p.name, "arch": getattr(p, "gcnArchName", ""), "memory_gib": round(p.total_memory / 2**30, 1),
+            "torch": torch.__version__, "hip": torch.version.hip, "python": platform.python_version()}
+
+
+def gemm_rate() -> float:
+    """TFLOP/s of a plain fp16 4096^3 matmul on the same timer (a GEMM-rate yardstick)."""
+    from .timing import do_bench
+
+    a, b = (torch.randn(4096, 4096, device="cuda", dtype=torch.float16) for _ in range(2))
+    return 2 * 4096**3 / (do_bench(lambda: a @ b) * 1e-3) / 1e12
+
+
+def table_picks(seqs: Iterable[int], dim: int) -> dict[str, dict[str, int]]:
+    from . import _lib
+
+    return {f"{n}/{mask}": {name: _lib.pick_config(kid, dim, _lib.F16, mask == "causal", n)
+                            for kid, name in _lib.KERNEL_NAMES.items()}
+            for n in seqs for mask in MASKS}
+
+
+def run(seqs: list[int], tokens: int, heads: int, dim: int, autotune: bool = False,
+        impls: list[Impl] | None = None) -> dict[str, Any]:
+    from . import autotune_cache, set_autotune
+
+    impls = impls if impls is not None else default_impls()
+    set_autotune(autotune)
+    inputs = {n: make_inputs(n, tokens, heads, dim, "cuda") for n in seqs}
+    cells = sweep_cells(impls, inputs, heads, dim, gpu_timer, after_cell=torch.cuda.empty_cache)
+    errors = measure_errors(impls, inputs)
     return {
-        "env": {
-            "gpu": props.name,
-            "arch": getattr(props, "gcnArchName", ""),
-            "memory_gib": round(props.total_memory / 2**30, 1),
-            "torch": torch.__version__,
-            "hip": torch.version.hip,
-            "python": platform.python_version(),
-        },
-        "config": {
+        "schema": "tattn-suite/1",
+        "device": device_info(),
+        "method": {
             "tokens": tokens, "heads": heads, "dim": dim, "dtype": "float16",
-            "timer": "tattn.timing.do_bench: 256 MB cache flush before each call, median, warm-up ~25 ms, rep ~100 ms",
+            "timer": "tattn.timing.do_bench: 256 MB cache flush before each call, median, ~25 ms warm-up, ~100 ms",
             "flops": "4*B*H*N^2*D (halved when causal); fwd+bwd = 3.5x fwd",
             "data": "N(0,1), device generator seeded with N (dO from the same generator)",
         },
-        "fp16_matmul_4096_tflops": 2 * 4096**3 / (mm_ms * 1e-3) / 1e12,
-        "rows": rows,
-        "accuracy": accuracy,
-        "table_picks": picks,
-        "tuned_configs": autotune_cache() if autotune else None,
+        "cells": cells,
+        "errors": errors,
+        "gemm_tflops": gemm_rate(),
+        "picks": table_picks(seqs, dim),
+        "autotuned": autotune_cache() if autotune else None,
     }
 
 
-def main() -> None:
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+def main(argv: list[str] | None = None) -> None:
+    ap = argparse.ArgumentParser(description="tattn against PyTorch's attention backends")
     ap.add_argument("--seqs", default="512,1024,2048,4096,8192,16384")
-    ap.add_argument("--tokens", type=int, default=16384, help="batch * seq held constant")
+    ap.add_argument("--tokens", type=int, default=16384, help="batch * seq per cell")
     ap.add_argument("--heads", type=int, default=16)
     ap.add_argument("--dim", type=int, default=64)
     ap.add_argument("--autotune", action="store_true", help="time the tile table on first use")
     ap.add_argument("--out", default=None)
-    a = ap.parse_args()
+    a = ap.parse_args(argv)
     if not torch.cuda.is_available():
         raise SystemExit("needs a ROCm GPU")
-    res = run([int(x) for x in a.seqs.split(",")], a.tokens, a.heads, a.dim, a.autotune)
-    name = res["env"]["arch"].split(":")[0] or res["env"]["gpu"].replace(" ", "_").lower()
-    out = Path(a.out) if a.out else REPO / "results" / f"{name}.json"
+    res = run([int(s) for s in a.seqs.split(",")], a.tokens, a.heads, a.dim, a.autotune)
+    arch = res["device"]["arch"].split(":")[0] or res["device"]["name"].replace(" ", "_").lower()
+    out = Path(a.out) if a.out else REPO / "results" / f"{arch}.json"
     out.parent.mkdir(parents=True, exist_ok=True)
-    out.write_text(json.dumps(res, indent=2) + "\n")
+    out.write_text(json.dumps(res, indent=1) + "\n")
     print("wrote", out)
 
 

@@ -58,7 +58,7 @@ def _inputs(n: int, dev):
     return b, q, k, v, do
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "fwd_pipe_traffic_fp16_d64_headline.md"
+TRAFFIC_FILE = ROOT / "profiles" / "fwd_persist_traffic_fp16_d64_headline.md"
 
 
 def measured_traffic() -> int | None:
@@ -269,18 +269,23 @@ def main() -> int:
     # Per shape: the table entry the forward runs, its average launch time and roofline fraction.
     from tattn import _lib
 
+    def entry_name(n: int) -> str:
+        cfg = _lib.config_desc(_lib.K_FWD, DIM, _lib.F16, _lib.pick_config(_lib.K_FWD, DIM, _lib.F16, a.causal, n))
+        kind = {2: f"fwd_persist_kernel, ring {cfg['ring']}", 1: "fwd_pipe_kernel"}.get(cfg["kind"], "fwd_generic_kernel")
+        return f"{kind}, {cfg['waves']} waves x {cfg['tiles']} tiles ({cfg['block_m']} query rows per workgroup)"
+
     per_n = []
     for n in seqs:
         ds = [e0.elapsed_time(e1) for m, e0, e1 in launch_events if m == n]
         f = flops(data[n][0], HEADS, n, DIM, a.causal, "fwd")
-        cfg = _lib.config_desc(_lib.K_FWD, DIM, _lib.F16, _lib.pick_config(_lib.K_FWD, DIM, _lib.F16, a.causal, n))
         tf = f / (sum(ds) / len(ds) * 1e-3) / 1e12
-        per_n.append({"seq": n, "batch": data[n][0], "entry": f"{cfg['waves']} waves x {cfg['tiles']} tiles "
-                      f"({cfg['block_m']} query rows per workgroup)", "avg_launch_us": round(1e3 * sum(ds) / len(ds), 2),
+        per_n.append({"seq": n, "batch": data[n][0], "entry": entry_name(n),
+                      "avg_launch_us": round(1e3 * sum(ds) / len(ds), 2),
                       "tflops": round(tf, 1), "frac": round(tf / PEAK_F16_TFLOPS, 4)})
+    names = sorted({entry_name(n) for n in seqs})
     roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                 "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic,
-                "kernel": f"tattn::fwd_pipe_kernel (fp16, D=64, {'causal' if a.causal else 'non-causal'})",
+                "kernel": f"tattn::{' / '.join(names)} (fp16, D=64, {'causal' if a.causal else 'non-causal'})",
                 "avg_launch_ms": kernel_ms, "launches": len(durations),
                 "flops_per_launch": fwd_flops / len(durations), "per_n": per_n}
 

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TATTN_ABI_VERSION 1
+#define TATTN_ABI_VERSION 2
 
 /* TATTN_BF16 has no counterpart in the reference, which accepts fp16 and fp32 only
  * (src/tattn/api.py:55-56); it runs the fp16 kernels with bf16 MFMAs and bf16 rounding points. */
@@ -47,7 +47,9 @@ typedef struct tattn_config {
   int32_t waves;        /* wavefronts (64 lanes) per workgroup */
   int32_t tiles;        /* 32-row MFMA tiles each wave owns */
   int32_t lds_bytes;    /* LDS the workgroup uses */
-  int32_t reserved;
+  int32_t kind;         /* 0 generic kernel, 1 software-pipelined, 2 persistent (falls back to the
+                           pipelined kernel of the same tiles where a problem does not fit it) */
+  int32_t ring;         /* persistent forward: K/V tiles in flight (LDS ring depth); else 0 */
 } tattn_config;
 
 /* ABI version of the loaded library; equals TATTN_ABI_VERSION of this header. */
@@ -129,7 +131,9 @@ int tattn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o
  * Tile table introspection (the gfx950 replacement of the reference's autotune config lists,
  * src/tattn/kernels.py:21-54): number of entries for (kernel, D, dtype), the entry itself, and
  * the entry the library picks for a problem (the reference keys its autotuner on
- * (N bucket, head dim, causal), kernels.py:57-61 and api.py:59-62).
+ * (N bucket, head dim, causal), kernels.py:57-61 and api.py:59-62). tattn_pick_config reports
+ * the pick for a batch x heads count that is a multiple of 8; the entry points also take the
+ * batch x heads count into account (the persistent forward needs whole slices per XCD).
  */
 int tattn_num_configs(int kernel, int64_t D, int dtype);
 int tattn_config_desc(int kernel, int64_t D, int dtype, int config_id, tattn_config* out);

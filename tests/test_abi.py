@@ -36,7 +36,7 @@ def test_header_constants_match_binding():
     text = HEADER.read_text()
     assert "TATTN_F16 = 0" in text and "TATTN_F32 = 1" in text
     assert "TATTN_K_FWD = 0" in text and "TATTN_K_BWD_DKDV = 1" in text and "TATTN_K_BWD_DQ = 2" in text
-    assert ctypes.sizeof(_lib.TattnConfig) == 24
+    assert ctypes.sizeof(_lib.TattnConfig) == 28
 
 
 @pytest.mark.parametrize("kernel", [_lib.K_FWD, _lib.K_BWD_DKDV, _lib.K_BWD_DQ])

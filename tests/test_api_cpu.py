@@ -69,6 +69,11 @@ def test_config_resolution():
     assert _resolve(_lib.K_FWD, 64, torch.float16, sel, False, 128) == 0
     with pytest.raises(ValueError, match="matches 0"):
         _resolve(_lib.K_FWD, 64, torch.float16, {"BLOCK_M": 7}, False, 128)
+    # A persistent entry shares its tiles with a pipelined one listed before it: "kind" picks it.
+    twin = dict(sel, kind=2)
+    pid = _resolve(_lib.K_FWD, 64, torch.float16, twin, False, 128)
+    desc = _lib.config_desc(_lib.K_FWD, 64, _lib.F16, pid)
+    assert pid > 0 and desc["kind"] == 2 and desc["block_m"] == first["block_m"] and desc["ring"] in (4, 8)
 
 
 def test_autotune_off_by_default_and_cache_format(monkeypatch):

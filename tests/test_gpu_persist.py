@@ -1,0 +1,96 @@
+"""The persistent forward entries of the tile table (kind 2) on shapes that meet their
+preconditions (Z*H a multiple of 8, N a multiple of the block and of 128, an even number of
+causal blocks per slice): O and M against float32 attention and against the pipelined kernel of
+the same tiles, from one work item per workgroup to several (the benchmark's 32 x 16 heads of
+512 tokens), fp16 and bf16, both masks. Shapes that do not fit run the pipelined kernel and are
+covered by tests/test_gpu_configs.py."""
+
+import math
+
+import pytest
+import torch
+
+from helpers import F16_MAX, check_max
+from oracle.reference import naive_attention
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+SHAPES = [(1, 8, 512), (2, 8, 1024), (4, 16, 2048), (1, 8, 4096), (32, 16, 512), (2, 4, 384), (8, 16, 256)]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from tattn import hip_available
+
+    assert hip_available(DEV), "libtattn_hip.so did not load or the device is not a gfx950"
+
+
+def _persistent_entries():
+    if not torch.cuda.is_available():
+        return []
+    from tattn import _lib
+
+    out = []
+    for c in range(_lib.num_configs(_lib.K_FWD, 64, _lib.F16)):
+        desc = _lib.config_desc(_lib.K_FWD, 64, _lib.F16, c)
+        if desc["kind"] == 2:
+            twin = next(t for t in range(_lib.num_configs(_lib.K_FWD, 64, _lib.F16))
+                        if _lib.config_desc(_lib.K_FWD, 64, _lib.F16, t)["kind"] == 1
+                        and (_lib.config_desc(_lib.K_FWD, 64, _lib.F16, t)["waves"],
+                             _lib.config_desc(_lib.K_FWD, 64, _lib.F16, t)["tiles"]) == (desc["waves"], desc["tiles"]))
+            out.append((c, twin))
+    return out
+
+
+def _reference(q, k, v, causal, scale):
+    z, h, n, _ = q.shape
+    per = max(1, (1 << 27) // (z * n * n))
+    o, m = [], []
+    for i in range(0, h, per):
+        qs, ks, vs = (t[:, i:i + per].float() for t in (q, k, v))
+        s = qs @ ks.transpose(-1, -2) * scale
+        if causal:
+            s = s.masked_fill(torch.ones(n, n, dtype=torch.bool, device=DEV).triu(1), float("-inf"))
+        m.append(torch.logsumexp(s, -1) / math.log(2.0))
+        o.append(torch.softmax(s, -1) @ vs)
+    return torch.cat(o, 1), torch.cat(m, 1)
+
+
+@pytest.mark.parametrize("entry", _persistent_entries(), ids=lambda e: f"cfg{e[0]}")
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_persistent_forward(entry, shape, causal, dtype):
+    from tattn.api import _forward
+
+    cid, twin = entry
+    b, h, n = shape
+    print(f"persistent fwd: cfg{cid} shape={shape} causal={causal} {dtype}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(n * 7 + b + int(causal))
+    q, k, v = (torch.randn(b, h, n, 64, device=DEV, dtype=dtype, generator=g) for _ in range(3))
+    o, m = _forward(q, k, v, causal, 0.125, config=cid)
+    o2, m2 = _forward(q, k, v, causal, 0.125, config=twin)
+    torch.cuda.synchronize()
+    want_o, want_m = _reference(q, k, v, causal, 0.125)
+    bound = F16_MAX if dtype == torch.float16 else 8 * F16_MAX
+    check_max(f"cfg{cid} {shape} causal={causal} {dtype} o", o, want_o, bound)
+    check_max(f"cfg{cid} {shape} causal={causal} {dtype} M", m, want_m, 1e-3 if dtype == torch.float16 else 8e-3)
+    # Same math as the pipelined kernel: equal up to the rounding of the softmax's lazy max moves.
+    torch.testing.assert_close(o.float(), o2.float(), atol=2 ** -10, rtol=2 ** -9)
+    torch.testing.assert_close(m, m2, atol=1e-4, rtol=0)
+
+
+def test_persistent_inference_path_and_repeat():
+    """M = NULL (inference) gives the same O; two calls in a row give the same bits."""
+    from tattn.api import _forward
+
+    cid = _persistent_entries()[0][0]
+    q, k, v = (torch.randn(4, 16, 1024, 64, device=DEV, dtype=torch.float16) for _ in range(3))
+    for causal in (False, True):
+        o1, _ = _forward(q, k, v, causal, 0.125, config=cid)
+        o2, m2 = _forward(q, k, v, causal, 0.125, config=cid, save_lse=False)
+        o3, _ = _forward(q, k, v, causal, 0.125, config=cid)
+        assert m2 is None and torch.equal(o1, o2) and torch.equal(o1, o3)

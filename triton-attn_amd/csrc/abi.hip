@@ -102,10 +102,17 @@ const TileEntry* config_entry(int kernel, int64_t D, int dtype, int id) {
 // on (sequence length, head dim, causal) (src/tattn/kernels.py:57-61), but static: the choices
 // below are the fastest entries measured on an MI355X at 16,384 tokens per batch, H=16. Entry 0
 // of each table is its general-purpose tile.
-int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N) {
+// ZH = Z * H: the persistent forward entries are picked where they run the problem themselves.
+int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N, int64_t ZH) {
   if (dtype == TATTN_F32) return 0;  // fp16 and bf16 share the picks
   switch (kernel) {
-    case TATTN_K_FWD:  // short rows: 128-row blocks; long: 256 rows (causal) or 512 rows
+    case TATTN_K_FWD:  // persistent where it fits (D=64); else 128-row blocks short, 256 / 512 long
+      if (D == 64) {
+        // Persistent 4 x 1 (causal) and 4 x 2 (non-causal), ring of 4: fastest at every benchmark
+        // length (cold-cache medians, 16,384 tokens x 16 heads).
+        const int pid = causal ? 5 : 7;
+        if (fwd_persist_fits(FwdTable<_Float16, 64>::e[pid], ZH, N, causal != 0)) return pid;
+      }
       if (D == 128) return 0;
       if (causal) return N >= 4096 ? 0 : 1;
       if (D == 64) return N >= 4096 ? 3 : N >= 1024 ? 0 : 1;
@@ -177,9 +184,9 @@ int check_shape(int64_t Z, int64_t H, int64_t N, int64_t D, int dtype) {
   return TATTN_OK;
 }
 
-int resolve(int kernel, int64_t D, int dtype, int causal, int64_t N, int id, int* out) {
+int resolve(int kernel, int64_t D, int dtype, int causal, int64_t N, int64_t ZH, int id, int* out) {
   const int n = num_configs(kernel, D, dtype);
-  if (id < 0) id = pick_config(kernel, D, dtype, causal, N);
+  if (id < 0) id = pick_config(kernel, D, dtype, causal, N, ZH);
   if (id >= n) return set_error(TATTN_E_CONFIG, "config id %d out of range [0, %d)", id, n);
   *out = id;
   return TATTN_OK;
@@ -208,7 +215,8 @@ int tattn_config_desc(int kernel, int64_t D, int dtype, int config_id, tattn_con
   const int rows = e->nw * e->tiles * 32;
   out->waves = e->nw;
   out->tiles = e->tiles;
-  out->reserved = 0;
+  out->kind = e->pipe;
+  out->ring = e->pipe == 2 ? e->ring : 0;
   if (kernel == TATTN_K_BWD_DKDV) {
     out->block_n = rows;
     out->block_m = e->other;
@@ -223,7 +231,7 @@ int tattn_config_desc(int kernel, int64_t D, int dtype, int config_id, tattn_con
 
 int tattn_pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N) {
   if (num_configs(kernel, D, dtype) < 0) return set_error(TATTN_E_ARG, "no table for kernel %d, D=%lld", kernel, (long long)D), -1;
-  return pick_config(kernel, D, dtype, causal, N);
+  return pick_config(kernel, D, dtype, causal, N, 8);  // any Z * H that is a multiple of 8
 }
 
 int tattn_fwd(const void* q, const void* k, const void* v, void* o, float* m, const int64_t q_strides[4],
@@ -238,7 +246,7 @@ int tattn_fwd(const void* q, const void* k, const void* v, void* o, float* m, co
     return rc;
   // m may be null: the log-sum-exp is then not stored (no backward will follow).
   int id;
-  if ((rc = resolve(TATTN_K_FWD, D, dtype, causal, N, config_id, &id))) return rc;
+  if ((rc = resolve(TATTN_K_FWD, D, dtype, causal, N, Z * H, config_id, &id))) return rc;
   if ((rc = device_check())) return rc;
   FwdParams p{};
   p.q = q; p.k = k; p.v = v; p.o = o; p.m = m;
@@ -288,7 +296,7 @@ int tattn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout
     return rc;
   if (!m || !delta) return set_error(TATTN_E_ARG, "m and delta must not be null");
   int id;
-  if ((rc = resolve(TATTN_K_BWD_DKDV, D, dtype, causal, N, config_id, &id))) return rc;
+  if ((rc = resolve(TATTN_K_BWD_DKDV, D, dtype, causal, N, Z * H, config_id, &id))) return rc;
   if ((rc = device_check())) return rc;
   p.q = q; p.k = k; p.v = v; p.dout = dout; p.dk = dk; p.dv = dv; p.m = m; p.delta = const_cast<float*>(delta);
   return launch_bwd_dkdv(p, (int)D, dtype, causal != 0, id, (hipStream_t)stream);
@@ -307,7 +315,7 @@ int tattn_bwd_dq(const void* q, const void* k, const void* v, const void* dout, 
     return rc;
   if (!m || !delta) return set_error(TATTN_E_ARG, "m and delta must not be null");
   int id;
-  if ((rc = resolve(TATTN_K_BWD_DQ, D, dtype, causal, N, config_id, &id))) return rc;
+  if ((rc = resolve(TATTN_K_BWD_DQ, D, dtype, causal, N, Z * H, config_id, &id))) return rc;
   if ((rc = device_check())) return rc;
   p.q = q; p.k = k; p.v = v; p.dout = dout; p.dq = dq; p.m = m; p.delta = const_cast<float*>(delta);
   return launch_bwd_dq(p, (int)D, dtype, causal != 0, id, (hipStream_t)stream);

@@ -61,8 +61,6 @@ __device__ __forceinline__ typename H16<T>::V8 lds8(const char* p) {
   return *reinterpret_cast<const TATTN_LDS typename H16<T>::V8*>((const TATTN_LDS char*)p);
 }
 
-template <int N> using IC = std::integral_constant<int, N>;
-
 // ---- dK / dV --------------------------------------------------------------------------------
 template <typename T, int D, int NW, int OCC, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams p) {

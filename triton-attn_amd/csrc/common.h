@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace tattn {
 
 typedef _Float16 f16;
@@ -32,6 +34,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 #define TATTN_LDS __attribute__((address_space(3)))
+
+template <int N> using IC = std::integral_constant<int, N>;
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -152,6 +156,8 @@ struct FwdParams {
   int32_t Z, H, N;
   int32_t n_qblocks;
   float c;  // sm_scale * log2(e)
+  int32_t items_x, gx;  // persistent kernel: work items per XCD, workgroups per XCD
+  int32_t cus;          // persistent kernel: compute units of the device
 };
 
 struct BwdParams {

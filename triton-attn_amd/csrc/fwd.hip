@@ -20,6 +20,7 @@
 // Causal: key steps entirely above the workgroup's last row are never loaded; steps entirely
 // above a wave's last row are skipped by that wave; only steps that cross the diagonal or the
 // sequence end pay for per-element masks (kernels.py:117-131).
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -735,7 +736,57 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_pipe_kernel(const FwdParams 
   }
 }
 
+}  // namespace tattn
+
+#include "fwd_persist.h"
+
+namespace tattn {
+
 // ---- launch ------------------------------------------------------------------------------
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Persistent forward: grid of one workgroup per resident slot (at most), the work split per XCD
+// into whole rounds. Returns 1 (nothing launched) when the problem does not meet the kernel's
+// preconditions.
+template <typename T, int D, int NW, int QT, int OCC, bool CAUSAL, int R>
+static int launch_fwd_persist(FwdParams p, hipStream_t st, int* rc) {
+  constexpr int BM = NW * QT * 32;
+  constexpr TileEntry self{NW, QT, 32, OCC, 2, R};
+  const int64_t S = (int64_t)p.Z * p.H;
+  if (!fwd_persist_fits(self, S, p.N, CAUSAL)) return 1;
+  const int nb = p.N / BM;
+  const int64_t items_x = S / 8 * (CAUSAL ? nb / 2 : nb);
+  if (items_x >= (1 << 30)) return 1;
+  static int per_cu = 0;  // resident workgroups per CU (same on every gfx950)
+  if (per_cu <= 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fwd_persist_kernel<T, D, NW, QT, OCC, CAUSAL, R>, NW * 64, 0) !=
+            hipSuccess || n <= 0)
+      n = 1;
+    per_cu = n;
+  }
+  p.cus = device_cus();
+  const int64_t slots_x = std::max<int64_t>(1, (int64_t)per_cu * p.cus / 8);
+  const int64_t rounds = (items_x + slots_x - 1) / slots_x;
+  p.n_qblocks = nb;
+  p.items_x = (int32_t)items_x;
+  p.gx = (int32_t)((items_x + rounds - 1) / rounds);
+  fwd_persist_kernel<T, D, NW, QT, OCC, CAUSAL, R><<<dim3(8u * (unsigned)p.gx), dim3(NW * 64), 0, st>>>(p);
+  *rc = check_launch("tattn_fwd");
+  return 0;
+}
 
 template <typename T, int D, int I>
 static int launch_fwd_entry(const FwdParams& p0, bool causal, hipStream_t st) {
@@ -758,6 +809,15 @@ static int launch_fwd_entry(const FwdParams& p0, bool causal, hipStream_t st) {
         fwd_generic_kernel<T, D, 4, 1, 64, false, D == 128 ? 1 : 2><<<dim3((unsigned)(((p.N + 127) / 128) * (int64_t)p.Z * p.H)), dim3(256), 0, st>>>(
             [&] { FwdParams q = p; q.n_qblocks = (p.N + 127) / 128; return q; }());
       return check_launch("tattn_fwd");
+    }
+    if constexpr (e.pipe == 2) {  // persistent, where the problem fits it
+      int rc = TATTN_OK;
+      if (causal) {
+        if constexpr (fwd_persist_causal_ok(e))
+          if (launch_fwd_persist<T, D, e.nw, e.tiles, e.occ, true, e.ring>(p0, st, &rc) == 0) return rc;
+      } else if (launch_fwd_persist<T, D, e.nw, e.tiles, e.occ, false, e.ring>(p0, st, &rc) == 0) {
+        return rc;
+      }
     }
     if (causal)
       fwd_pipe_kernel<T, D, e.nw, e.tiles, e.occ, true><<<grid, block, 0, st>>>(p);
@@ -812,6 +872,10 @@ int launch_fwd(const FwdParams& p, int D, int dtype, bool causal, int id, hipStr
 }
 
 int fwd_lds_bytes(int D, int dtype, const TileEntry& e) {
+  if ((dtype == 0 || dtype == 2) && e.pipe == 2) {
+    const int slot = 32 * (D < 32 ? 64 : 2 * D);
+    return 2 * e.ring * slot;
+  }
   if (dtype == 0 || dtype == 2) {
     switch (D) {
       case 16: return PipeLayout<16>::LDS;

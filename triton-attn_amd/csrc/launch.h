@@ -28,6 +28,21 @@ int launch_bwd_dkdv(const BwdParams& p, int D, int dtype, bool causal, int confi
 int launch_bwd_dq(const BwdParams& p, int D, int dtype, bool causal, int config_id, hipStream_t st);
 
 int fwd_lds_bytes(int D, int dtype, const TileEntry& e);
+
+// Whether a persistent forward entry (kind 2) runs a problem itself; otherwise the launcher runs
+// the pipelined kernel of the same tiles. Z*H a multiple of 8 (whole slices per XCD), N a
+// multiple of the block and of the ring period (whole unrolled groups), causal: an even number
+// of blocks per slice (pairs), a diagonal region of one or two ring periods, and one 32-row tile
+// per wave (the causal kernel with two tiles per wave needs more than the 256 registers a wave
+// has at two waves per SIMD; those entries run their pipelined twin for causal problems).
+constexpr bool fwd_persist_causal_ok(const TileEntry& e) {
+  return e.tiles == 1 && (e.nw * e.tiles) % e.ring == 0 && e.nw * e.tiles / e.ring <= 2;
+}
+inline bool fwd_persist_fits(const TileEntry& e, int64_t ZH, int64_t N, bool causal) {
+  const int64_t bm = (int64_t)e.nw * e.tiles * 32;
+  if (e.pipe != 2 || ZH % 8 != 0 || N % bm != 0 || N % (32 * e.ring) != 0) return false;
+  return !causal || ((N / bm) % 2 == 0 && fwd_persist_causal_ok(e));
+}
 int dkdv_lds_bytes(int D, int dtype, const TileEntry& e);
 int dq_lds_bytes(int D, int dtype, const TileEntry& e);
 

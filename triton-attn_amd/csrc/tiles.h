@@ -19,7 +19,8 @@ struct TileEntry {
   int tiles;  // 32-row MFMA tiles per wave (queries for fwd/dQ, keys for dK/dV)
   int other;  // keys per step (fwd, dQ) or queries per step (dK/dV)
   int occ;    // waves per SIMD the kernel is compiled for (register budget 512 / occ)
-  int pipe;   // 1: software-pipelined 16-bit kernel, 0: generic kernel
+  int pipe;   // 2: persistent 16-bit kernel, 1: software-pipelined 16-bit kernel, 0: generic kernel
+  int ring = 4;  // persistent forward: LDS ring depth (K/V tiles), 4 or 8
 };
 
 // ---- forward ----------------------------------------------------------------------------
@@ -42,7 +43,8 @@ template <typename T, int D> struct FwdTable;
 // wave per SIMD (512 registers). Of the fp32 kernels only causal dK/dV at D=128 spills (32 bytes).
 TATTN_TABLE16(FwdTable, 16, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1})
 TATTN_TABLE16(FwdTable, 32, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1})
-TATTN_TABLE16(FwdTable, 64, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {8, 2, 32, 2, 1})
+TATTN_TABLE16(FwdTable, 64, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {8, 2, 32, 2, 1},
+              {4, 2, 32, 2, 2, 8}, {4, 1, 32, 2, 2, 4}, {8, 1, 32, 2, 2, 8}, {4, 2, 32, 2, 2, 4})
 TATTN_TABLE16(FwdTable, 128, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1})
 TATTN_TABLE(FwdTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(FwdTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})

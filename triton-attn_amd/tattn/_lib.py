@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library is loaded, see above)
 
 LIB_PATH = Path(__file__).resolve().with_name("libtattn_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F16, F32, BF16 = 0, 1, 2
 K_FWD, K_BWD_DKDV, K_BWD_DQ = 0, 1, 2
@@ -34,7 +34,8 @@ class TattnConfig(ctypes.Structure):
         ("waves", ctypes.c_int32),
         ("tiles", ctypes.c_int32),
         ("lds_bytes", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("kind", ctypes.c_int32),
+        ("ring", ctypes.c_int32),
     ]
 
 
@@ -134,7 +135,7 @@ def config_desc(kernel: int, d: int, dtype: int, cid: int) -> dict[str, int]:
     out = TattnConfig()
     check(load().tattn_config_desc(kernel, d, dtype, cid, ctypes.byref(out)), "tattn_config_desc")
     return {"id": cid, "block_m": out.block_m, "block_n": out.block_n, "waves": out.waves,
-            "tiles": out.tiles, "lds_bytes": out.lds_bytes}
+            "tiles": out.tiles, "lds_bytes": out.lds_bytes, "kind": out.kind, "ring": out.ring}
 
 
 def pick_config(kernel: int, d: int, dtype: int, causal: bool, n: int) -> int:

@@ -103,8 +103,10 @@ def _kernel_layout(t: torch.Tensor) -> torch.Tensor:
 
 def _resolve(kernel: int, d: int, dtype: torch.dtype, config: Config, causal: bool, n: int) -> int:
     """Maps the reference-style `config=` to a table index: None -> the library's pick; an int is
-    the index; a dict may give "id" or any of block_m / block_n / waves / tiles (upper-case
-    BLOCK_M / BLOCK_N as in the reference are accepted) and must match exactly one entry."""
+    the index; a dict may give "id" or any of block_m / block_n / waves / tiles / kind / ring
+    (upper-case BLOCK_M / BLOCK_N as in the reference are accepted) and must match at least one
+    entry; of several, the lowest index (a persistent entry, kind 2, shares its tiles with the
+    pipelined entry listed before it: give "kind": 2 to select it)."""
     if config is None:
         return -1
     if isinstance(config, int):
@@ -112,12 +114,12 @@ def _resolve(kernel: int, d: int, dtype: torch.dtype, config: Config, causal: bo
     if "id" in config:
         return int(config["id"])
     want = {k.lower(): int(v) for k, v in config.items()
-            if k.lower() in ("block_m", "block_n", "waves", "tiles")}
+            if k.lower() in ("block_m", "block_n", "waves", "tiles", "kind", "ring")}
     code = _DTYPES[dtype]
     hits = [c for c in range(_lib.num_configs(kernel, d, code))
             if all(_lib.config_desc(kernel, d, code, c)[key] == val for key, val in want.items())]
-    if len(hits) != 1:
-        raise ValueError(f"config {config} matches {len(hits)} {_lib.KERNEL_NAMES[kernel]} table entries")
+    if not hits:
+        raise ValueError(f"config {config} matches 0 {_lib.KERNEL_NAMES[kernel]} table entries")
     return hits[0]
 
 

@@ -94,3 +94,63 @@ def test_persistent_inference_path_and_repeat():
         o2, m2 = _forward(q, k, v, causal, 0.125, config=cid, save_lse=False)
         o3, _ = _forward(q, k, v, causal, 0.125, config=cid)
         assert m2 is None and torch.equal(o1, o2) and torch.equal(o1, o3)
+
+
+def _bwd_entries(kernel):
+    if not torch.cuda.is_available():
+        return []
+    from tattn import _lib
+
+    k = {"dkdv": _lib.K_BWD_DKDV, "dq": _lib.K_BWD_DQ}[kernel]
+    descs = [_lib.config_desc(k, 64, _lib.F16, c) for c in range(_lib.num_configs(k, 64, _lib.F16))]
+    out = []
+    for d in descs:
+        if d["kind"] == 2:
+            twin = next(t for t in descs if t["kind"] == 1 and t["waves"] == d["waves"])
+            out.append((kernel, d["id"], twin["id"]))
+    return out
+
+
+BWD_SHAPES = [(1, 8, 512), (32, 16, 512), (16, 16, 1024), (2, 8, 2048), (8, 16, 256), (2, 4, 384)]
+
+
+@pytest.mark.parametrize("entry", _bwd_entries("dkdv") + _bwd_entries("dq"), ids=lambda e: f"{e[0]}{e[1]}")
+@pytest.mark.parametrize("shape", BWD_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_persistent_backward_matches_pipelined(entry, shape, causal, dtype):
+    """The persistent dK/dV and dQ kernels give the bits of the pipelined kernel with the same
+    waves (same summation order and rounding points), from one block per workgroup to several,
+    both masks; shapes that do not fit them run the pipelined kernel (same bits trivially)."""
+    from tattn.api import _backward, _forward
+
+    kernel, pid, twin = entry
+    b, h, n = shape
+    print(f"persistent bwd: {kernel}{pid} shape={shape} causal={causal} {dtype}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(n * 3 + b + int(causal))
+    q, k, v, do = (torch.randn(b, h, n, 64, device=DEV, dtype=dtype, generator=g) for _ in range(4))
+    o, m = _forward(q, k, v, causal, 0.125)
+    got = _backward(q, k, v, o, m, do, causal, 0.125, config={kernel: pid})
+    want = _backward(q, k, v, o, m, do, causal, 0.125, config={kernel: twin})
+    torch.cuda.synchronize()
+    for name, a, w in zip(("dq", "dk", "dv"), got, want):
+        assert torch.equal(a, w), f"{name} differs from the pipelined kernel"
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_persistent_backward_against_float32(causal):
+    """The library's picks at the benchmark shape (16 x 16 heads of 1,024 tokens) against float32
+    autograd, flat envelope (causal gradients: the documented cap)."""
+    from helpers import F16_CAUSAL_GRAD_MAX
+    from tattn import attention
+
+    g = torch.Generator(device=DEV).manual_seed(1024 + int(causal))
+    q, k, v, do = (torch.randn(16, 16, 1024, 64, device=DEV, dtype=torch.float16, generator=g) for _ in range(4))
+    qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+    attention(qg, kg, vg, causal=causal).backward(do)
+    for i in range(0, 16, 4):
+        qs, ks, vs = (t[i:i + 4].float().requires_grad_() for t in (q, k, v))
+        naive_attention(qs, ks, vs, causal=causal).backward(do[i:i + 4].float())
+        for name, got, want in (("dq", qg.grad[i:i + 4], qs.grad), ("dk", kg.grad[i:i + 4], ks.grad),
+                                ("dv", vg.grad[i:i + 4], vs.grad)):
+            check_max(f"batch {i}: {name} causal={causal}", got, want, F16_CAUSAL_GRAD_MAX if causal else F16_MAX)

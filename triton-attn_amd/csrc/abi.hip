@@ -121,8 +121,9 @@ int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N, int64_t
       if (D != 64) return 0;  // D=128: entry 0 is pipelined at one wave per SIMD (512 registers)
       if (!causal) return 1;
       return N >= 2048 ? 1 : N >= 1024 ? 0 : 2;
-    case TATTN_K_BWD_DQ:  // 4 waves, except non-causal 2048 <= N < 8192 (8 waves, up to 2% faster)
+    case TATTN_K_BWD_DQ:  // persistent 4 waves where it fits; else 4 waves (8 for non-causal 2048 <= N < 8192)
       if (D != 64) return 0;
+      if (bwd_persist_fits(DqTable<_Float16, 64>::e[5], ZH, N, causal != 0)) return 5;
       return !causal && N >= 2048 && N < 8192 ? 1 : 0;
   }
   return 0;
@@ -302,9 +303,11 @@ int tattn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout
   return launch_bwd_dkdv(p, (int)D, dtype, causal != 0, id, (hipStream_t)stream);
 }
 
-int tattn_bwd_dq(const void* q, const void* k, const void* v, const void* dout, void* dq, const float* m,
-                 const float* delta, const int64_t strides[4], int64_t Z, int64_t H, int64_t N, int64_t D,
-                 int dtype, int causal, float sm_scale, int config_id, void* stream) {
+// dQ; with o_fused (O, in the shared layout) the kernel computes delta = rowsum(dO * O) itself, in
+// the preprocess's order, and stores it into `delta` for the dK/dV kernel that follows.
+static int bwd_dq_call(const void* q, const void* k, const void* v, const void* dout, void* dq, const float* m,
+                       const float* delta, const int64_t strides[4], int64_t Z, int64_t H, int64_t N, int64_t D,
+                       int dtype, int causal, float sm_scale, int config_id, void* stream, const void* o_fused) {
   BwdParams p{};
   int rc;
   if ((rc = bwd_common(p, strides, Z, H, N, D, dtype, sm_scale))) return rc;
@@ -318,7 +321,18 @@ int tattn_bwd_dq(const void* q, const void* k, const void* v, const void* dout, 
   if ((rc = resolve(TATTN_K_BWD_DQ, D, dtype, causal, N, Z * H, config_id, &id))) return rc;
   if ((rc = device_check())) return rc;
   p.q = q; p.k = k; p.v = v; p.dout = dout; p.dq = dq; p.m = m; p.delta = const_cast<float*>(delta);
+  if (o_fused) {
+    p.o = o_fused;
+    p.fuse_delta = 1;
+  }
   return launch_bwd_dq(p, (int)D, dtype, causal != 0, id, (hipStream_t)stream);
+}
+
+int tattn_bwd_dq(const void* q, const void* k, const void* v, const void* dout, void* dq, const float* m,
+                 const float* delta, const int64_t strides[4], int64_t Z, int64_t H, int64_t N, int64_t D,
+                 int dtype, int causal, float sm_scale, int config_id, void* stream) {
+  return bwd_dq_call(q, k, v, dout, dq, m, delta, strides, Z, H, N, D, dtype, causal, sm_scale, config_id, stream,
+                     nullptr);
 }
 
 int tattn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, void* dq, void* dk,
@@ -330,6 +344,26 @@ int tattn_bwd(const void* q, const void* k, const void* v, const void* o, const 
     // One id for both kernels, as the reference's `config=` (api.py:124-145): it must exist in both tables.
     if (config_id >= num_configs(TATTN_K_BWD_DKDV, D, dtype) || config_id >= num_configs(TATTN_K_BWD_DQ, D, dtype))
       return set_error(TATTN_E_CONFIG, "config id %d out of range for the backward tables", config_id);
+  }
+  // When dQ runs a pipelined 16-bit kernel it computes delta itself (same bits as the preprocess)
+  // and stores it: dQ, then dK/dV, two launches and no separate pass over dO. Otherwise
+  // preprocess, dK/dV, dQ.
+  bool fuse = false;
+  {
+    BwdParams p{};
+    int qid;
+    if ((rc = bwd_common(p, strides, Z, H, N, D, dtype, sm_scale))) return rc;
+    if ((rc = resolve(TATTN_K_BWD_DQ, D, dtype, causal, N, Z * H, dq_id, &qid))) return rc;
+    const TileEntry* e = config_entry(TATTN_K_BWD_DQ, D, dtype, qid);
+    fuse = dtype != TATTN_F32 && e && e->pipe >= 1 && bwd_fits32(p, (int)D);
+  }
+  if (fuse) {
+    const int sz = dtype == TATTN_F32 ? 4 : 2;
+    if ((rc = check_tensor("o", o, strides, sz))) return rc;
+    if (!delta) return set_error(TATTN_E_ARG, "delta is a null pointer");
+    if ((rc = bwd_dq_call(q, k, v, dout, dq, m, delta, strides, Z, H, N, D, dtype, causal, sm_scale, dq_id, stream, o)))
+      return rc;
+    return tattn_bwd_dkdv(q, k, v, dout, dk, dv, m, delta, strides, Z, H, N, D, dtype, causal, sm_scale, dk_id, stream);
   }
   if ((rc = tattn_bwd_preprocess(o, dout, delta, strides, Z, H, N, D, dtype, stream))) return rc;
   if ((rc = tattn_bwd_dkdv(q, k, v, dout, dk, dv, m, delta, strides, Z, H, N, D, dtype, causal, sm_scale, dk_id,

@@ -352,7 +352,18 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
     }
   }
   const float nm = -(q < N ? p.m[(int64_t)zh * N + q] : 0.0f);
-  const float dl = q < N ? p.delta[(int64_t)zh * N + q] : 0.0f;
+  float dl;
+  if (p.fuse_delta) {  // delta = rowsum(dO * O) here, stored for the dK/dV kernel that follows
+    float sd[NSD];
+    const int64_t off = hoff + (int64_t)(q < N ? q : 0) * rs + 8 * h2;
+#pragma unroll
+    for (int s = 0; s < NSD; ++s) sd[s] = chunk_dot(*reinterpret_cast<const V8*>((const T*)p.o + off + 16 * s), dop[s]);
+    dl = row_delta(sd);
+    if (q >= N) dl = 0.0f;
+    else if (h2 == 0) p.delta[(int64_t)zh * N + q] = dl;
+  } else {
+    dl = q < N ? p.delta[(int64_t)zh * N + q] : 0.0f;
+  }
   // -delta of the lane's query in every register: seeds the dP^T accumulator, so the MFMAs
   // return dP - delta.
   f32x16 ndl;

@@ -118,6 +118,30 @@ template <> struct H16<bf16> {
   }
 };
 
+// Dot product of one 16-byte chunk of O and dO in float32: one FMA chain in element order. The
+// delta preprocess and the dQ kernels that compute delta themselves both use it, and both then
+// add chunk sums in the same butterfly order, so every path gives delta the same bits.
+template <typename V8>
+__device__ __forceinline__ float chunk_dot(V8 x, V8 y) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc = __builtin_fmaf((float)x[i], (float)y[i], acc);
+  return acc;
+}
+
+// delta of a row from the chunk sums a lane holds when lane-half h2 owns chunks 2k + h2
+// (k < NS) of it, in the preprocess's order: chunk sums paired CPR/2, CPR/4, ..., 1 chunks
+// apart (CPR = 2 NS chunks per row), the last pair being the two lane-halves.
+template <int NS>
+__device__ __forceinline__ float row_delta(float (&s)[NS]) {
+#pragma unroll
+  for (int off = NS / 2; off >= 1; off >>= 1)
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+      if ((k & off) == 0 && k + off < NS) s[k] = s[k] + s[k + off];
+  return sum_halves(s[0]);
+}
+
 // Key permutation inside a 32-row tile: swaps bits 2 and 3 of the row index. Storing key r of
 // a tile at LDS row perm32(r) makes the MFMA C layout hand every lane-half 8 consecutive keys
 // per 16-key slice: C register r of lane-half h then holds key kappa(r, h).
@@ -176,6 +200,8 @@ struct BwdParams {
   int32_t n_blocks;
   float c;      // sm_scale * log2(e)
   float scale;  // sm_scale
+  int32_t items_x, gx, cus;  // persistent kernels: items per XCD, workgroups per XCD, CUs
+  int32_t fuse_delta;        // dQ computes delta from O and dO itself and stores it (no preprocess)
 };
 
 // Bytes spanned by rows [0, N) of a row-strided slice: every offset of a valid element is below

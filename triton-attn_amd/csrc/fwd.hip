@@ -744,19 +744,6 @@ namespace tattn {
 
 // ---- launch ------------------------------------------------------------------------------
 
-// Compute units of the current device (cached per device).
-static int device_cus() {
-  static int cus[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] <= 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
 // Persistent forward: grid of one workgroup per resident slot (at most), the work split per XCD
 // into whole rounds. Returns 1 (nothing launched) when the problem does not meet the kernel's
 // preconditions.

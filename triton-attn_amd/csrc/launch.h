@@ -29,6 +29,34 @@ int launch_bwd_dq(const BwdParams& p, int D, int dtype, bool causal, int config_
 
 int fwd_lds_bytes(int D, int dtype, const TileEntry& e);
 
+// Whether the backward's (z, h) slices fit 32-bit buffer offsets (plus two steps of look-ahead):
+// the pipelined and persistent backward kernels need it, the generic ones take 64-bit addresses.
+inline bool bwd_fits32(const BwdParams& p, int D) {
+  return slice_bytes(p.N, p.s[2], D) + (uint64_t)p.s[2] * 128 < (1ull << 31);
+}
+
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Whether a persistent backward entry (kind 2) runs a problem itself; otherwise the launcher
+// runs the pipelined kernel of the same waves. Z*H a multiple of 8, N a multiple of the block
+// and of 128 (whole groups of four steps), causal: an even number of blocks per slice (pairs).
+inline bool bwd_persist_fits(const TileEntry& e, int64_t ZH, int64_t N, bool causal) {
+  const int64_t blk = (int64_t)e.nw * 32;
+  if (e.pipe != 2 || ZH % 8 != 0 || N % blk != 0 || N % 128 != 0) return false;
+  return !causal || (N / blk) % 2 == 0;
+}
+
 // Whether a persistent forward entry (kind 2) runs a problem itself; otherwise the launcher runs
 // the pipelined kernel of the same tiles. Z*H a multiple of 8 (whole slices per XCD), N a
 // multiple of the block and of the ring period (whole unrolled groups), causal: an even number

@@ -70,7 +70,8 @@ TATTN_TABLE(DkdvTable, float, 128, {4, 1, 32, 1, 0})
 template <typename T, int D> struct DqTable;
 TATTN_TABLE16(DqTable, 16, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0})
 TATTN_TABLE16(DqTable, 32, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0})
-TATTN_TABLE16(DqTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {8, 1, 64, 2, 0})
+TATTN_TABLE16(DqTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {8, 1, 64, 2, 0},
+              {4, 1, 32, 2, 2}, {8, 1, 32, 2, 2})
 TATTN_TABLE16(DqTable, 128, {4, 1, 32, 1, 1}, {4, 1, 32, 1, 0})
 TATTN_TABLE(DqTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DqTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})

@@ -649,12 +649,12 @@ static int launch_dkdv_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(e.nw * 64);
   if constexpr (e.pipe >= 1) {
-    static_assert(sizeof(T) == 2 && D <= 128 && e.tiles == 1 && e.other == 32, "pipelined dK/dV shape");
+    static_assert(sizeof(T) == 2 && D <= 128 && (e.tiles == 1 || D <= 64) && e.other == 32, "pipelined dK/dV shape");
     if (slice_fits32(p, D)) {
       if (causal)
-        dkdv_pipe_kernel<T, D, e.nw, e.occ, true><<<grid, block, 0, st>>>(p);
+        dkdv_pipe_kernel<T, D, e.nw, e.tiles, e.occ, true><<<grid, block, 0, st>>>(p);
       else
-        dkdv_pipe_kernel<T, D, e.nw, e.occ, false><<<grid, block, 0, st>>>(p);
+        dkdv_pipe_kernel<T, D, e.nw, e.tiles, e.occ, false><<<grid, block, 0, st>>>(p);
       return check_launch("tattn_bwd_dkdv");
     }
     p.n_blocks = (p.N + 127) / 128;  // slices beyond 2 GiB: 64-bit addressing

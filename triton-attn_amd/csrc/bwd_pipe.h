@@ -62,14 +62,18 @@ __device__ __forceinline__ typename H16<T>::V8 lds8(const char* p) {
 }
 
 // ---- dK / dV --------------------------------------------------------------------------------
-template <typename T, int D, int NW, int OCC, bool CAUSAL>
+// KT key tiles per wave (32 KT keys): every Q / dO operand a wave reads from LDS (natural for S
+// and dP, transposed for dK and dV) feeds KT MFMAs, so LDS bytes per MFMA fall by KT. KT = 2
+// needs about 400 registers (K and V operands, dK and dV accumulators and the S / dP pairs of
+// both tiles) and runs at one wave per SIMD.
+template <typename T, int D, int NW, int KT, int OCC, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams p) {
   using H = H16<T>;
   using V8 = typename H::V8;
   using V4 = typename H::V4;
   using V2 = typename H::V2;
   using B = BwdPipe<D>;
-  constexpr int NT = NW * 64, BNK = NW * 32;
+  constexpr int NT = NW * 64, BNK = NW * KT * 32;
   constexpr int STAGE = B::DKDV_STAGE;
   constexpr int CPT = (B::CHUNKS + NT - 1) / NT;
   constexpr int NSD = B::NSD, DT = B::DT;
@@ -85,26 +89,29 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
   const int64_t rs = p.s[2];
   const float c = p.c;
   const int kblk = kbi * BNK;
-  const int kw0 = kblk + 32 * w;
+  const int kw0 = kblk + 32 * KT * w;  // first key of the wave; tile kt holds keys kw0 + 32 kt + l32
   // Causal: query blocks below this key block never see its keys (kernels.py:206-208).
   const int lo = CAUSAL ? kblk : 0;
   const int nsteps = (N - lo + 31) / 32;
 
-  V8 kop[NSD], vop[NSD];
-  {
-    const int key = kw0 + l32;
+  V8 kop[KT][NSD], vop[KT][NSD];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    const int key = kw0 + 32 * kt + l32;
     const int64_t off = hoff + (int64_t)(key < N ? key : 0) * rs + 8 * h2;
 #pragma unroll
     for (int s = 0; s < NSD; ++s) {
       const V8 a = *reinterpret_cast<const V8*>((const T*)p.k + off + 16 * s);
       const V8 b = *reinterpret_cast<const V8*>((const T*)p.v + off + 16 * s);
-      kop[s] = key < N ? a : V8{};
-      vop[s] = key < N ? b : V8{};
+      kop[kt][s] = key < N ? a : V8{};
+      vop[kt][s] = key < N ? b : V8{};
     }
   }
-  f32x16 dk[DT], dv[DT];
+  f32x16 dk[KT][DT], dv[KT][DT];
 #pragma unroll
-  for (int u = 0; u < DT; ++u) dk[u] = dv[u] = f32x16{};
+  for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+    for (int u = 0; u < DT; ++u) dk[kt][u] = dv[kt][u] = f32x16{};
 
   // HBM: Q, dO rows and M, delta entries from query `lo` on.
   const __amdgpu_buffer_rsrc_t qrs = slice_rsrc((const T*)p.q + hoff + (int64_t)lo * rs, slice_bytes(N - lo, rs, D));
@@ -161,28 +168,39 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
     if (md_loader) *reinterpret_cast<uint32_t*>(base + md_dst) = (tid & 32) ? (pdl ^ 0x80000000u) : pm;
   };
 
-  // S = Q K^T and dP - delta = dO V^T - delta of the stage's 32 queries (C layout: lane = key,
-  // register r = query kappa(r, h2)); the dP chain starts from the stage's -delta.
-  auto qk = [&](f32x16& s, f32x16& dp, int st) {
+  // S = Q K^T and dP - delta = dO V^T - delta of the stage's 32 queries for each key tile (C
+  // layout: lane = key, register r = query kappa(r, h2)); the dP chains start from the stage's
+  // -delta. Each Q / dO operand read from LDS feeds the KT tiles.
+  auto qk = [&](f32x16 (&s)[KT], f32x16 (&dp)[KT], int st) {
     const char* base = smem + st * STAGE;
-    s = f32x16{};
     {
       const TATTN_LDS char* nd = (const TATTN_LDS char*)base + mo + 128;
       const f32x4 n0 = *reinterpret_cast<const TATTN_LDS f32x4*>(nd);
       const f32x4 n1 = *reinterpret_cast<const TATTN_LDS f32x4*>(nd + 16);
       const f32x4 n2 = *reinterpret_cast<const TATTN_LDS f32x4*>(nd + 64);
       const f32x4 n3 = *reinterpret_cast<const TATTN_LDS f32x4*>(nd + 80);
-      dp = f32x16{n0[0], n0[1], n0[2], n0[3], n1[0], n1[1], n1[2], n1[3],
-                  n2[0], n2[1], n2[2], n2[3], n3[0], n3[1], n3[2], n3[3]};
+      const f32x16 nd16 = f32x16{n0[0], n0[1], n0[2], n0[3], n1[0], n1[1], n1[2], n1[3],
+                                 n2[0], n2[1], n2[2], n2[3], n3[0], n3[1], n3[2], n3[3]};
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        s[kt] = f32x16{};
+        dp[kt] = nd16;
+      }
     }
 #pragma unroll
     for (int sd = 0; sd < NSD; ++sd) {
-      s = Elt<T>::mfma(lds8<T>(base + nat[sd]), kop[sd], s);
-      dp = Elt<T>::mfma(lds8<T>(base + B::TILE + nat[sd]), vop[sd], dp);
+      const V8 qa = lds8<T>(base + nat[sd]);
+      const V8 oa = lds8<T>(base + B::TILE + nat[sd]);
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        s[kt] = Elt<T>::mfma(qa, kop[kt][sd], s[kt]);
+        dp[kt] = Elt<T>::mfma(oa, vop[kt][sd], dp[kt]);
+      }
     }
   };
-  // dV += P^T dO, dK += dS^T Q over the stage's 32 queries.
-  auto grad_mma = [&](const V8* pp, const V8* dsp, int st) {
+  // dV += P^T dO, dK += dS^T Q over the stage's 32 queries (each transposed operand feeds the KT
+  // tiles).
+  auto grad_mma = [&](const V8 (&pp)[KT][2], const V8 (&dsp)[KT][2], int st) {
     const char* base = smem + st * STAGE;
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl)
@@ -191,41 +209,48 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
         V8 dob = tr_pair<T>(base + B::TILE, tra[sl][u][0], tra[sl][u][1]);
         V8 qb = tr_pair<T>(base, tra[sl][u][0], tra[sl][u][1]);
         if (D < 32 && 16 * ((lane >> 4) & 1) >= D) dob = qb = V8{};
-        dv[u] = Elt<T>::mfma(pp[sl], dob, dv[u]);
-        dk[u] = Elt<T>::mfma(dsp[sl], qb, dk[u]);
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+          dv[kt][u] = Elt<T>::mfma(pp[kt][sl], dob, dv[kt][u]);
+          dk[kt][u] = Elt<T>::mfma(dsp[kt][sl], qb, dk[kt][u]);
+        }
       }
   };
   // P = exp2(S c - M), dS = P (dP - delta) for the stage's queries, rounded into MFMA operands
   // (dp already holds dP - delta).
-  auto pds = [&](const f32x16& s, const f32x16& dp, V8* pp, V8* dsp, int st, int q0, auto mask_tag) {
+  auto pds = [&](const f32x16 (&s)[KT], const f32x16 (&dp)[KT], V8 (&pp)[KT][2], V8 (&dsp)[KT][2], int st, int q0,
+                 auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const char* base = smem + st * STAGE;
-    const int key = kw0 + l32;
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
       const f32x4 m0 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 64 * a);
       const f32x4 m1 = *reinterpret_cast<const TATTN_LDS f32x4*>((const TATTN_LDS char*)base + mo + 64 * a + 16);
-      V8 x, y;
 #pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        float pr[2], dr[2];
+      for (int kt = 0; kt < KT; ++kt) {
+        const int key = kw0 + 32 * kt + l32;
+        V8 x, y;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int r = 8 * a + i + e;
-          const float mv = (i + e) < 4 ? m0[i + e] : m1[i + e - 4];
-          float pv = fast_exp2(__builtin_fmaf(s[r], c, -mv));
-          if constexpr (MASK) pv = key > q0 + kappa(r, h2) ? 0.0f : pv;
-          pr[e] = pv;
-          dr[e] = pv * dp[r];
+        for (int i = 0; i < 8; i += 2) {
+          float pr[2], dr[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int r = 8 * a + i + e;
+            const float mv = (i + e) < 4 ? m0[i + e] : m1[i + e - 4];
+            float pv = fast_exp2(__builtin_fmaf(s[kt][r], c, -mv));
+            if constexpr (MASK) pv = key > q0 + kappa(r, h2) ? 0.0f : pv;
+            pr[e] = pv;
+            dr[e] = pv * dp[kt][r];
+          }
+          const V2 ph = H::pack(pr[0], pr[1]), dh = H::pack(dr[0], dr[1]);
+          x[i] = ph[0];
+          x[i + 1] = ph[1];
+          y[i] = dh[0];
+          y[i + 1] = dh[1];
         }
-        const V2 ph = H::pack(pr[0], pr[1]), dh = H::pack(dr[0], dr[1]);
-        x[i] = ph[0];
-        x[i + 1] = ph[1];
-        y[i] = dh[0];
-        y[i + 1] = dh[1];
+        pp[kt][a] = x;
+        dsp[kt][a] = y;
       }
-      pp[a] = x;
-      dsp[a] = y;
     }
   };
 
@@ -243,13 +268,16 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
     }
   __syncthreads();
 
-  f32x16 sa, da, sb, db;
-  V8 pa[2] = {}, dsa[2] = {}, pb[2], dsb[2];
+  f32x16 sa[KT], da[KT], sb[KT], db[KT];
+  V8 pa[KT][2], dsa[KT][2], pb[KT][2], dsb[KT][2];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) pa[kt][0] = pa[kt][1] = dsa[kt][0] = dsa[kt][1] = V8{};
   qk(sa, da, 0);
 
   // One step: S/dP of step i+1, dV/dK of step i-1, P/dS of step i; ST = i % 4 (or -1: run time).
-  auto step = [&](int i, int st, f32x16& scur, f32x16& dcur, f32x16& snext, f32x16& dnext,
-                  const V8* pprev, const V8* dsprev, V8* pcur, V8* dscur, auto mask_tag) {
+  auto step = [&](int i, int st, f32x16 (&scur)[KT], f32x16 (&dcur)[KT], f32x16 (&snext)[KT], f32x16 (&dnext)[KT],
+                  const V8 (&pprev)[KT][2], const V8 (&dsprev)[KT][2], V8 (&pcur)[KT][2], V8 (&dscur)[KT][2],
+                  auto mask_tag) {
     gload(i + 2);
     qk(snext, dnext, (st + 1) & 3);
     grad_mma(pprev, dsprev, (st + 3) & 3);
@@ -258,29 +286,34 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
     __syncthreads();
   };
   auto roll = [&]() {  // next becomes current
-    sa = sb;
-    da = db;
-    pa[0] = pb[0];
-    pa[1] = pb[1];
-    dsa[0] = dsb[0];
-    dsa[1] = dsb[1];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      sa[kt] = sb[kt];
+      da[kt] = db[kt];
+      pa[kt][0] = pb[kt][0];
+      pa[kt][1] = pb[kt][1];
+      dsa[kt][0] = dsb[kt][0];
+      dsa[kt][1] = dsb[kt][1];
+    }
   };
 
   int i = 0;
-  // Causal: the workgroup's first NW query blocks cross its keys' diagonal; mask them. Query
-  // block i < w lies wholly before wave w's keys (P = dS = 0): the wave skips its MFMAs and
-  // softmax there and only stages tiles, leaving its SIMD to the other waves.
-  const int n_mask = CAUSAL ? min(nsteps, NW) : 0;
+  // Causal: the workgroup's first NW KT query blocks cross its keys' diagonal; mask them. Query
+  // block i below KT w lies wholly before wave w's keys (P = dS = 0): the wave skips its MFMAs
+  // and softmax there and only stages tiles, leaving its SIMD to the other waves. (With KT = 2
+  // the wave's second tile sees no key of block KT w either; the mask zeroes it.)
+  const int wt = KT * w;
+  const int n_mask = CAUSAL ? min(nsteps, NW * KT) : 0;
   for (; i < n_mask; ++i) {
     gload(i + 2);
-    if (i + 1 >= w) qk(sb, db, (i + 1) & 3);
-    if (i - 1 >= w) grad_mma(pa, dsa, (i + 3) & 3);
-    if (i >= w) pds(sa, da, pb, dsb, i & 3, lo + 32 * i, std::true_type{});
+    if (i + 1 >= wt) qk(sb, db, (i + 1) & 3);
+    if (i - 1 >= wt) grad_mma(pa, dsa, (i + 3) & 3);
+    if (i >= wt) pds(sa, da, pb, dsb, i & 3, lo + 32 * i, std::true_type{});
     lstore((i + 2) & 3);
     __syncthreads();
     roll();
   }
-  for (; i + 3 < nsteps; i += 4) {  // i % 4 == 0 here (NW is a multiple of 4)
+  for (; i + 3 < nsteps; i += 4) {  // i % 4 == 0 here (NW KT is a multiple of 4)
     step(i, 0, sa, da, sb, db, pa, dsa, pb, dsb, std::false_type{});
     step(i + 1, 1, sb, db, sa, da, pb, dsb, pa, dsa, std::false_type{});
     step(i + 2, 2, sa, da, sb, db, pa, dsa, pb, dsb, std::false_type{});
@@ -292,23 +325,25 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
   }
   grad_mma(pa, dsa, (nsteps - 1) & 3);
 
-  // Store: C register r of lane holds key 8*(r/4) + 4*h2 + r%4 of the wave, column 32u + l32.
+  // Store: C register r of lane holds key 8*(r/4) + 4*h2 + r%4 of the tile, column 32u + l32.
   T* DK = (T*)p.dk + hoff;
   T* DV = (T*)p.dv + hoff;
 #pragma unroll
-  for (int u = 0; u < DT; ++u) {
-    const int d = 32 * u + l32;
-    if (d < D) {
+  for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kw0 + 8 * (r >> 2) + 4 * h2 + (r & 3);
-        if (key < N) {
-          DK[(int64_t)key * rs + d] = (T)(dk[u][r] * p.scale);
-          DV[(int64_t)key * rs + d] = (T)dv[u][r];
+    for (int u = 0; u < DT; ++u) {
+      const int d = 32 * u + l32;
+      if (d < D) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kw0 + 32 * kt + 8 * (r >> 2) + 4 * h2 + (r & 3);
+          if (key < N) {
+            DK[(int64_t)key * rs + d] = (T)(dk[kt][u][r] * p.scale);
+            DV[(int64_t)key * rs + d] = (T)dv[kt][u][r];
+          }
         }
       }
     }
-  }
 }
 
 // ---- dQ ----------------------------------------------------------------------------------

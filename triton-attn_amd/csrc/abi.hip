@@ -117,10 +117,10 @@ int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N, int64_t
       if (causal) return N >= 4096 ? 0 : 1;
       if (D == 64) return N >= 4096 ? 3 : N >= 1024 ? 0 : 1;
       return D == 16 && N < 2048 ? 1 : 0;
-    case TATTN_K_BWD_DKDV:  // pipelined, 4 waves (128 keys) or 8 waves (256 keys); causal N < 1024: generic
+    case TATTN_K_BWD_DKDV:  // pipelined, 8 waves (256 keys); causal N < 2048: 4 waves (128 keys)
       if (D != 64) return 0;  // D=128: entry 0 is pipelined at one wave per SIMD (512 registers)
       if (!causal) return 1;
-      return N >= 2048 ? 1 : N >= 1024 ? 0 : 2;
+      return N >= 2048 ? 1 : 0;
     case TATTN_K_BWD_DQ:  // persistent 4 waves where it fits; else 4 waves (8 for non-causal 2048 <= N < 8192)
       if (D != 64) return 0;
       if (bwd_persist_fits(DqTable<_Float16, 64>::e[5], ZH, N, causal != 0)) return 5;

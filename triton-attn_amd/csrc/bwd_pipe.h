@@ -143,29 +143,33 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
     for (int u = 0; u < DT; ++u) tr_addrs<D>(sl, u, lane, tra[sl][u][0], tra[sl][u][1]);
   const int mo = 2 * B::TILE + 32 * h2;  // M of queries 8*h2.. (bytes); delta at +128
 
-  u32x4 pq[CPT], pd[CPT];
-  uint32_t pm, pdl;
-  auto gload = [&](int step) {
+  // Register stage of one step's Q, dO, M and delta (the loop uses set 0; the prologue also
+  // set 1, so both of its steps are in flight at once).
+  u32x4 pq[2][CPT], pd[2][CPT];
+  uint32_t pm[2], pdl[2];
+  auto gload = [&](int step, auto set_tag) {
+    constexpr int R = decltype(set_tag)::value;
     const uint32_t so = (uint32_t)step * step_bytes;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      pq[i] = rsrc_load(qrs, goff[i] + so);
-      pd[i] = rsrc_load(ors, goff[i] + so);
+      pq[R][i] = rsrc_load(qrs, goff[i] + so);
+      pd[R][i] = rsrc_load(ors, goff[i] + so);
     }
     const uint32_t mo4 = (uint32_t)(((tid & 31) + 32 * step) * 4);
-    pm = __builtin_amdgcn_raw_buffer_load_b32(mrs, (int)mo4, 0, 0);
-    pdl = __builtin_amdgcn_raw_buffer_load_b32(drs, (int)mo4, 0, 0);
+    pm[R] = __builtin_amdgcn_raw_buffer_load_b32(mrs, (int)mo4, 0, 0);
+    pdl[R] = __builtin_amdgcn_raw_buffer_load_b32(drs, (int)mo4, 0, 0);
   };
-  auto lstore = [&](int st) {
+  auto lstore = [&](int st, auto set_tag) {
+    constexpr int R = decltype(set_tag)::value;
     char* base = smem + st * STAGE;
 #pragma unroll
     for (int i = 0; i < CPT; ++i)
       if (B::CHUNKS % NT == 0 || tid + i * NT < B::CHUNKS) {
-        st16(base + ldst[i], pq[i]);
-        st16(base + B::TILE + ldst[i], pd[i]);
+        st16(base + ldst[i], pq[R][i]);
+        st16(base + B::TILE + ldst[i], pd[R][i]);
       }
     // delta is staged negated: it seeds the dP accumulator, so dP - delta comes out of the MFMAs.
-    if (md_loader) *reinterpret_cast<uint32_t*>(base + md_dst) = (tid & 32) ? (pdl ^ 0x80000000u) : pm;
+    if (md_loader) *reinterpret_cast<uint32_t*>(base + md_dst) = (tid & 32) ? (pdl[R] ^ 0x80000000u) : pm[R];
   };
 
   // S = Q K^T and dP - delta = dO V^T - delta of the stage's 32 queries for each key tile (C
@@ -254,18 +258,18 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
     }
   };
 
-  // Prologue: steps 0 and 1 into stages 0 and 1; stage 3 (read by step 0 together with
-  // all-zero P and dS) cleared.
-  gload(0);
-  lstore(0);
-  gload(1);
-  lstore(1);
+  // Prologue: steps 0 and 1 into stages 0 and 1, both loads in flight together (with the K/V
+  // operand loads above); stage 3 (read by step 0 together with all-zero P and dS) cleared.
+  gload(0, IC<0>{});
+  gload(1, IC<1>{});
 #pragma unroll
   for (int i = 0; i < CPT; ++i)
     if (B::CHUNKS % NT == 0 || tid + i * NT < B::CHUNKS) {
       st16(smem + 3 * STAGE + ldst[i], u32x4{0, 0, 0, 0});
       st16(smem + 3 * STAGE + B::TILE + ldst[i], u32x4{0, 0, 0, 0});
     }
+  lstore(0, IC<0>{});
+  lstore(1, IC<1>{});
   __syncthreads();
 
   f32x16 sa[KT], da[KT], sb[KT], db[KT];
@@ -278,11 +282,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
   auto step = [&](int i, int st, f32x16 (&scur)[KT], f32x16 (&dcur)[KT], f32x16 (&snext)[KT], f32x16 (&dnext)[KT],
                   const V8 (&pprev)[KT][2], const V8 (&dsprev)[KT][2], V8 (&pcur)[KT][2], V8 (&dscur)[KT][2],
                   auto mask_tag) {
-    gload(i + 2);
+    gload(i + 2, IC<0>{});
     qk(snext, dnext, (st + 1) & 3);
     grad_mma(pprev, dsprev, (st + 3) & 3);
     pds(scur, dcur, pcur, dscur, st, lo + 32 * i, mask_tag);
-    lstore((st + 2) & 3);
+    lstore((st + 2) & 3, IC<0>{});
     __syncthreads();
   };
   auto roll = [&]() {  // next becomes current
@@ -305,11 +309,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
   const int wt = KT * w;
   const int n_mask = CAUSAL ? min(nsteps, NW * KT) : 0;
   for (; i < n_mask; ++i) {
-    gload(i + 2);
+    gload(i + 2, IC<0>{});
     if (i + 1 >= wt) qk(sb, db, (i + 1) & 3);
     if (i - 1 >= wt) grad_mma(pa, dsa, (i + 3) & 3);
     if (i >= wt) pds(sa, da, pb, dsb, i & 3, lo + 32 * i, std::true_type{});
-    lstore((i + 2) & 3);
+    lstore((i + 2) & 3, IC<0>{});
     __syncthreads();
     roll();
   }
@@ -325,25 +329,47 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
   }
   grad_mma(pa, dsa, (nsteps - 1) & 3);
 
-  // Store: C register r of lane holds key 8*(r/4) + 4*h2 + r%4 of the tile, column 32u + l32.
+  // Store through LDS: C register r of lane holds key 8*(r/4) + 4*h2 + r%4 of the tile, column
+  // 32u + l32, so direct stores would write 2 bytes per lane and instruction. Each wave instead
+  // writes its tile into a private LDS block (row-major [key][d], RB bytes per row) and stores
+  // whole 16-byte chunks of rows. The blocks reuse the ring: the barrier waits until every
+  // wave's last reads of it are done.
+  __syncthreads();
+  constexpr int RB = B::RB;
+  constexpr int CPRO = D / 8;                 // 16-byte chunks per output row
+  constexpr int SPW = (32 * CPRO + 63) / 64;  // chunk stores per lane and tile
+  static_assert(NW * 32 * RB <= B::NST * STAGE, "store blocks fit the ring");
+  char* wb = smem + w * 32 * RB;
   T* DK = (T*)p.dk + hoff;
   T* DV = (T*)p.dv + hoff;
+  // The lane index is recomputed here (mbcnt) rather than kept live across the main loop, which
+  // runs at the register limit.
+  const int ln = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int l32e = ln & 31, h2e = ln >> 5;
+  auto store_tile = [&](const f32x16 (&acc)[DT], float mul, T* dst, int key0) {
+    TATTN_LDS T* wl = (TATTN_LDS T*)((TATTN_LDS char*)wb + 4 * h2e * RB) + l32e;
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt)
+    for (int u = 0; u < DT; ++u)
+      if (32 * u + l32e < D) {
 #pragma unroll
-    for (int u = 0; u < DT; ++u) {
-      const int d = 32 * u + l32;
-      if (d < D) {
+        for (int r = 0; r < 16; ++r) wl[(8 * (r >> 2) + (r & 3)) * (RB / 2) + 32 * u] = (T)(acc[u][r] * mul);
+      }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kw0 + 32 * kt + 8 * (r >> 2) + 4 * h2 + (r & 3);
-          if (key < N) {
-            DK[(int64_t)key * rs + d] = (T)(dk[kt][u][r] * p.scale);
-            DV[(int64_t)key * rs + d] = (T)dv[kt][u][r];
-          }
-        }
+    for (int it = 0; it < SPW; ++it) {
+      const int j = ln + 64 * it;
+      const int row = j / CPRO, cc = j % CPRO;
+      const int key = key0 + row;
+      if (row < 32 && key < N) {
+        const u32x4 v = *reinterpret_cast<const TATTN_LDS u32x4*>((const TATTN_LDS char*)wb + row * RB + 16 * cc);
+        st16(dst + (int64_t)key * rs + 8 * cc, v);
       }
     }
+  };
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    store_tile(dk[kt], p.scale, DK, kw0 + 32 * kt);
+    store_tile(dv[kt], 1.0f, DV, kw0 + 32 * kt);
+  }
 }
 
 // ---- dQ ----------------------------------------------------------------------------------
@@ -436,22 +462,26 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
 #pragma unroll
     for (int u = 0; u < DT; ++u) tr_addrs<D>(sl, u, lane, tra[sl][u][0], tra[sl][u][1]);
 
-  u32x4 pk[CPT], pv[CPT];
-  auto gload = [&](int step) {
+  // Register stage of one step's K and V (the loop uses set 0; the prologue also set 1, so both
+  // of its steps are in flight at once).
+  u32x4 pk[2][CPT], pv[2][CPT];
+  auto gload = [&](int step, auto set_tag) {
+    constexpr int R = decltype(set_tag)::value;
     const uint32_t so = (uint32_t)step * step_bytes;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      pk[i] = rsrc_load(krs, goff[i] + so);
-      pv[i] = rsrc_load(vrs, goff[i] + so);
+      pk[R][i] = rsrc_load(krs, goff[i] + so);
+      pv[R][i] = rsrc_load(vrs, goff[i] + so);
     }
   };
-  auto lstore = [&](int st) {
+  auto lstore = [&](int st, auto set_tag) {
+    constexpr int R = decltype(set_tag)::value;
     char* base = smem + st * STAGE;
 #pragma unroll
     for (int i = 0; i < CPT; ++i)
       if (B::CHUNKS % NT == 0 || tid + i * NT < B::CHUNKS) {
-        st16(base + ldst[i], pk[i]);
-        st16(base + B::TILE + ldst[i], pv[i]);
+        st16(base + ldst[i], pk[R][i]);
+        st16(base + B::TILE + ldst[i], pv[R][i]);
       }
   };
   // S^T = K Q^T and dP^T - delta = V dO^T - delta of the stage's 32 keys (C layout: lane = query,
@@ -504,13 +534,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
     }
   };
 
-  gload(0);
-  lstore(0);
-  gload(1);
-  lstore(1);
+  gload(0, IC<0>{});
+  gload(1, IC<1>{});
 #pragma unroll
   for (int i = 0; i < CPT; ++i)
     if (B::CHUNKS % NT == 0 || tid + i * NT < B::CHUNKS) st16(smem + 3 * STAGE + ldst[i], u32x4{0, 0, 0, 0});
+  lstore(0, IC<0>{});
+  lstore(1, IC<1>{});
   __syncthreads();
 
   f32x16 sa, da, sb, db;
@@ -519,11 +549,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
 
   auto full_step = [&](int i, int st, f32x16& scur, f32x16& dcur, f32x16& snext, f32x16& dnext,
                        const V8* eprev, V8* ecur) {
-    gload(i + 2);
+    gload(i + 2, IC<0>{});
     qk(snext, dnext, (st + 1) & 3);
     dq_mma(eprev, (st + 3) & 3);
     dsv(scur, dcur, ecur, 32 * i, std::false_type{});
-    lstore((st + 2) & 3);
+    lstore((st + 2) & 3, IC<0>{});
     __syncthreads();
   };
 
@@ -536,7 +566,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
   }
   // Remaining steps (masked or not): state scur = sa, eprev = ea.
   for (; i < nsteps; ++i) {
-    gload(i + 2);
+    gload(i + 2, IC<0>{});
     if (i - 1 < wave_steps) dq_mma(ea, (i + 3) & 3);
     if (i < wave_steps) {
       qk(sb, db, (i + 1) & 3);
@@ -549,7 +579,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_pipe_kernel(const BwdParams p
       ea[0] = eb[0];
       ea[1] = eb[1];
     }
-    lstore((i + 2) & 3);
+    lstore((i + 2) & 3, IC<0>{});
     __syncthreads();
   }
   if (wave_steps == nsteps && nsteps > 0) dq_mma(ea, (nsteps - 1) & 3);

@@ -48,7 +48,8 @@ typedef struct tattn_config {
   int32_t tiles;        /* 32-row MFMA tiles each wave owns */
   int32_t lds_bytes;    /* LDS the workgroup uses */
   int32_t kind;         /* 0 generic kernel, 1 software-pipelined, 2 persistent (falls back to the
-                           pipelined kernel of the same tiles where a problem does not fit it) */
+                           pipelined kernel of the same tiles where a problem does not fit it),
+                           3 dK/dV with paired waves (two waves per 32-key tile, split roles) */
   int32_t ring;         /* persistent forward: K/V tiles in flight (LDS ring depth); else 0 */
 } tattn_config;
 

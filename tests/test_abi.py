@@ -48,7 +48,9 @@ def test_tables_are_described(kernel, d, dtype):
     for c in range(n):
         desc = _lib.config_desc(kernel, d, dtype, c)
         assert desc["waves"] in (4, 8) and desc["tiles"] in (1, 2)
-        rows = desc["waves"] * desc["tiles"] * 32
+        # Paired-wave backward entries (kind 3) give each 32-row tile two waves.
+        rows = (desc["waves"] // 2 if desc["kind"] == 3 else desc["waves"]) * desc["tiles"] * 32
+        assert desc["kind"] in (0, 1, 2, 3) and (desc["kind"] != 3 or kernel != _lib.K_FWD)
         own = desc["block_n"] if kernel == _lib.K_BWD_DKDV else desc["block_m"]
         assert own == rows
         assert 0 < desc["lds_bytes"] <= 160 * 1024

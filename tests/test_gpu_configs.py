@@ -85,3 +85,54 @@ def test_autotune_first_use_times_once_and_stays_correct(monkeypatch):
         assert len(cache[kernel]) == 2
         for cid in cache[kernel].values():
             assert 0 <= cid < real(kid, 64, _lib.F16)
+
+
+def _raw_backward(kernel, q, k, v, do, m, delta, causal, cid):
+    """One dK/dV or dQ launch through the C ABI with a given table entry."""
+    from tattn import _lib
+
+    lib = _lib.load()
+    b, h, n, d = q.shape
+    code = {torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}[q.dtype]
+    _, (st,) = _lib.stride_block(q)
+    stream = torch.cuda.current_stream().cuda_stream
+    if kernel == "bwd_dkdv":
+        dk, dv = torch.empty_like(k), torch.empty_like(v)
+        _lib.check(lib.tattn_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), dk.data_ptr(),
+                                      dv.data_ptr(), m.data_ptr(), delta.data_ptr(), st, b, h, n, d, code,
+                                      int(causal), 0.125, cid, stream), "tattn_bwd_dkdv")
+        return dk, dv
+    dq = torch.empty_like(q)
+    _lib.check(lib.tattn_bwd_dq(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), dq.data_ptr(),
+                                m.data_ptr(), delta.data_ptr(), st, b, h, n, d, code, int(causal), 0.125,
+                                cid, stream), "tattn_bwd_dq")
+    return (dq,)
+
+
+@pytest.mark.parametrize("kernel", ["bwd_dkdv", "bwd_dq"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_paired_wave_entries_match_pipelined_bitwise(kernel, d, dtype):
+    """The paired-wave backward entries (kind 3: two waves per 32-row tile, one computing P, the
+    other dS and the gradient) keep the pipelined kernels' rounding points and summation order:
+    their gradients equal the 4-wave pipelined entry's bit for bit, on ragged and full lengths,
+    both masks."""
+    from tattn import _lib
+    from tattn.api import _forward
+
+    kid = _lib.K_BWD_DKDV if kernel == "bwd_dkdv" else _lib.K_BWD_DQ
+    descs = [_lib.config_desc(kid, d, _lib.F16, c) for c in range(_lib.num_configs(kid, d, _lib.F16))]
+    split = [x["id"] for x in descs if x["kind"] == 3]
+    pipe = [x["id"] for x in descs if x["kind"] == 1 and x["waves"] == 4 and x["tiles"] == 1][0]
+    assert split, "no paired-wave entry"
+    for (b, h, n) in [(1, 3, 1), (2, 3, 17), (2, 3, 70), (2, 4, 300), (1, 8, 1024), (4, 16, 512)]:
+        for causal in (False, True):
+            q, k, v, do = (rand((b, h, n, d), dtype, 13 * n + s, DEV) for s in range(4))
+            o, m = _forward(q, k, v, causal, 0.125)
+            delta = (o.float() * do.float()).sum(-1).contiguous()
+            want = _raw_backward(kernel, q, k, v, do, m, delta, causal, pipe)
+            for cid in split:
+                got = _raw_backward(kernel, q, k, v, do, m, delta, causal, cid)
+                for g, w in zip(got, want):
+                    assert torch.equal(g, w), (f"{kernel} entry {cid} vs {pipe} {(b, h, n, d)} causal={causal}: "
+                                               f"max diff {(g.float() - w.float()).abs().max().item():.3e}")

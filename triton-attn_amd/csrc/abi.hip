@@ -118,10 +118,12 @@ int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N, int64_t
       if (D == 64) return N >= 4096 ? 3 : N >= 1024 ? 0 : 1;
       return D == 16 && N < 2048 ? 1 : 0;
     case TATTN_K_BWD_DKDV:  // pipelined, 8 waves (256 keys); causal N < 2048: 4 waves (128 keys)
-      if (D != 64) return 0;  // D=128: entry 0 is pipelined at one wave per SIMD (512 registers)
+      if (D == 128) return 2;  // paired waves: two per SIMD, where one wave per tile needs all 512 registers
+      if (D != 64) return 0;
       if (!causal) return 1;
       return N >= 2048 ? 1 : 0;
     case TATTN_K_BWD_DQ:  // persistent 4 waves where it fits; else 4 waves (8 for non-causal 2048 <= N < 8192)
+      if (D == 128) return 2;  // paired waves, as dK/dV
       if (D != 64) return 0;
       if (bwd_persist_fits(DqTable<_Float16, 64>::e[5], ZH, N, causal != 0)) return 5;
       return !causal && N >= 2048 && N < 8192 ? 1 : 0;
@@ -213,7 +215,7 @@ int tattn_config_desc(int kernel, int64_t D, int dtype, int config_id, tattn_con
   const TileEntry* e = config_entry(kernel, D, dtype, config_id);
   if (!e) return set_error(TATTN_E_CONFIG, "no config %d for kernel %d, D=%lld, dtype %d", config_id, kernel,
                            (long long)D, dtype);
-  const int rows = e->nw * e->tiles * 32;
+  const int rows = tile_rows(*e);
   out->waves = e->nw;
   out->tiles = e->tiles;
   out->kind = e->pipe;

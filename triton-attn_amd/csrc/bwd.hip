@@ -23,6 +23,7 @@
 
 #include "bwd_persist.h"
 #include "bwd_pipe.h"
+#include "bwd_split.h"
 #include "common.h"
 #include "launch.h"
 #include "tiles.h"
@@ -642,13 +643,28 @@ static int launch_bwd_persist(BwdParams p, hipStream_t st) {
 template <typename T, int D, int I>
 static int launch_dkdv_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   constexpr TileEntry e = DkdvTable<T, D>::e[I];
-  constexpr int BNK = e.nw * e.tiles * 32;
+  constexpr int BNK = tile_rows(e);
   BwdParams p = p0;
   p.n_blocks = (p.N + BNK - 1) / BNK;
   const int64_t blocks = (int64_t)p.n_blocks * p.Z * p.H;
   if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(e.nw * 64);
-  if constexpr (e.pipe >= 1) {
+  if constexpr (e.pipe == 3) {  // paired waves, 128 keys per workgroup
+    static_assert(sizeof(T) == 2 && e.nw == 8 && e.tiles == 1 && e.other == 32, "paired-wave dK/dV shape");
+    if (slice_fits32(p, D)) {
+      if (causal)
+        dkdv_split_kernel<T, D, true><<<grid, block, 0, st>>>(p);
+      else
+        dkdv_split_kernel<T, D, false><<<grid, block, 0, st>>>(p);
+      return check_launch("tattn_bwd_dkdv");
+    }
+    p.n_blocks = (p.N + 127) / 128;  // slices beyond 2 GiB: 64-bit addressing
+    const dim3 g2((unsigned)((int64_t)p.n_blocks * p.Z * p.H));
+    if (causal)
+      dkdv_kernel<T, D, 4, 1, 32, true, D == 128 ? 1 : 2><<<g2, dim3(256), 0, st>>>(p);
+    else
+      dkdv_kernel<T, D, 4, 1, 32, false, D == 128 ? 1 : 2><<<g2, dim3(256), 0, st>>>(p);
+  } else if constexpr (e.pipe >= 1) {
     static_assert(sizeof(T) == 2 && D <= 128 && (e.tiles == 1 || D <= 64) && e.other == 32, "pipelined dK/dV shape");
     if (slice_fits32(p, D)) {
       if (causal)
@@ -675,13 +691,28 @@ static int launch_dkdv_entry(const BwdParams& p0, bool causal, hipStream_t st) {
 template <typename T, int D, int I>
 static int launch_dq_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   constexpr TileEntry e = DqTable<T, D>::e[I];
-  constexpr int BMQ = e.nw * e.tiles * 32;
+  constexpr int BMQ = tile_rows(e);
   BwdParams p = p0;
   p.n_blocks = (p.N + BMQ - 1) / BMQ;
   const int64_t blocks = (int64_t)p.n_blocks * p.Z * p.H;
   if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(e.nw * 64);
-  if constexpr (e.pipe >= 1) {
+  if constexpr (e.pipe == 3) {  // paired waves, 128 queries per workgroup
+    static_assert(sizeof(T) == 2 && e.nw == 8 && e.tiles == 1 && e.other == 32, "paired-wave dQ shape");
+    if (slice_fits32(p, D)) {
+      if (causal)
+        dq_split_kernel<T, D, true><<<grid, block, 0, st>>>(p);
+      else
+        dq_split_kernel<T, D, false><<<grid, block, 0, st>>>(p);
+      return check_launch("tattn_bwd_dq");
+    }
+    p.n_blocks = (p.N + 127) / 128;  // slices beyond 2 GiB: 64-bit addressing
+    const dim3 g2((unsigned)((int64_t)p.n_blocks * p.Z * p.H));
+    if (causal)
+      dq_kernel<T, D, 4, 1, 32, true, D == 128 ? 1 : 2><<<g2, dim3(256), 0, st>>>(p);
+    else
+      dq_kernel<T, D, 4, 1, 32, false, D == 128 ? 1 : 2><<<g2, dim3(256), 0, st>>>(p);
+  } else if constexpr (e.pipe >= 1) {
     static_assert(sizeof(T) == 2 && D <= 128 && e.tiles == 1 && e.other == 32, "pipelined dQ shape");
     if constexpr (e.pipe == 2) {
       if (slice_fits32(p, D) && bwd_persist_fits(e, (int64_t)p.Z * p.H, p.N, causal))
@@ -761,12 +792,14 @@ int launch_bwd_dq(const BwdParams& p, int D, int dtype, bool causal, int id, hip
 
 int dkdv_lds_bytes(int D, int dtype, const TileEntry& e) {
   const int r = dtype != 1 ? (D < 32 ? 64 : 2 * D) : 4 * D + 16;
+  if (e.pipe == 3) return 4 * (2 * 32 * r + 256) + 2 * 4 * 32 * 32 * 4;  // ring + P exchange buffers
   if (e.pipe) return 4 * (2 * 32 * r + 256);
   return 2 * (2 * e.other * r + 2 * e.other * 4);
 }
 
 int dq_lds_bytes(int D, int dtype, const TileEntry& e) {
   const int r = dtype != 1 ? (D < 32 ? 64 : 2 * D) : 4 * D + 16;
+  if (e.pipe == 3) return 4 * (2 * 32 * r) + 2 * 4 * 32 * 32 * 4;  // ring + P exchange buffers
   if (e.pipe) return 4 * (2 * 32 * r);
   return 2 * (2 * e.other * r);
 }

@@ -19,9 +19,14 @@ struct TileEntry {
   int tiles;  // 32-row MFMA tiles per wave (queries for fwd/dQ, keys for dK/dV)
   int other;  // keys per step (fwd, dQ) or queries per step (dK/dV)
   int occ;    // waves per SIMD the kernel is compiled for (register budget 512 / occ)
-  int pipe;   // 2: persistent 16-bit kernel, 1: software-pipelined 16-bit kernel, 0: generic kernel
+  int pipe;   // 3: backward with paired waves (split roles), 2: persistent 16-bit kernel,
+              // 1: software-pipelined 16-bit kernel, 0: generic kernel
   int ring = 4;  // persistent forward: LDS ring depth (K/V tiles), 4 or 8
 };
+
+// Rows (queries, or keys for dK/dV) one workgroup owns. The paired-wave backward kernels give
+// each 32-row tile two waves, one per role.
+constexpr int tile_rows(const TileEntry& e) { return (e.pipe == 3 ? e.nw / 2 : e.nw) * e.tiles * 32; }
 
 // ---- forward ----------------------------------------------------------------------------
 template <typename T, int D> struct FwdTable;
@@ -59,8 +64,8 @@ namespace tattn {
 template <typename T, int D> struct DkdvTable;
 TATTN_TABLE16(DkdvTable, 16, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {4, 2, 32, 2, 0})
 TATTN_TABLE16(DkdvTable, 32, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {4, 2, 32, 2, 0})
-TATTN_TABLE16(DkdvTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 32, 2, 0}, {4, 2, 32, 1, 1})
-TATTN_TABLE16(DkdvTable, 128, {4, 1, 32, 1, 1}, {4, 1, 32, 1, 0})
+TATTN_TABLE16(DkdvTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 32, 2, 0}, {4, 2, 32, 1, 1}, {8, 1, 32, 2, 3})
+TATTN_TABLE16(DkdvTable, 128, {4, 1, 32, 1, 1}, {4, 1, 32, 1, 0}, {8, 1, 32, 2, 3})
 TATTN_TABLE(DkdvTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DkdvTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DkdvTable, float, 64, {4, 1, 32, 2, 0})
@@ -71,8 +76,8 @@ template <typename T, int D> struct DqTable;
 TATTN_TABLE16(DqTable, 16, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0})
 TATTN_TABLE16(DqTable, 32, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 2, 32, 2, 0}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0})
 TATTN_TABLE16(DqTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {8, 1, 64, 2, 0},
-              {4, 1, 32, 2, 2}, {8, 1, 32, 2, 2})
-TATTN_TABLE16(DqTable, 128, {4, 1, 32, 1, 1}, {4, 1, 32, 1, 0})
+              {4, 1, 32, 2, 2}, {8, 1, 32, 2, 2}, {8, 1, 32, 2, 3})
+TATTN_TABLE16(DqTable, 128, {4, 1, 32, 1, 1}, {4, 1, 32, 1, 0}, {8, 1, 32, 2, 3})
 TATTN_TABLE(DqTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DqTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DqTable, float, 64, {4, 1, 32, 2, 0})

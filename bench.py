@@ -17,6 +17,7 @@ both masks, dq/dk/dv max abs error against float32 autograd at N = 1024 and 4096
 baseline: the oracle's tiled forward timed on the host cores on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline] [--no-accuracy]
+       (profiling: --no-sweep --seqs N --causal --backward --head-dim D)
 """
 
 from __future__ import annotations
@@ -164,6 +165,7 @@ def accuracy(data) -> list[dict]:
 
 
 def main() -> int:
+    global DIM
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
@@ -176,9 +178,12 @@ def main() -> int:
     ap.add_argument("--causal", action="store_true", help="headline step with the causal mask")
     ap.add_argument("--backward", action="store_true",
                     help="headline step runs forward + backward (for profiling the backward kernels)")
+    ap.add_argument("--head-dim", type=int, default=DIM, choices=(16, 32, 64, 128),
+                    help="head dim of every shape (default 64, the benchmark's; others for profiling)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB, 5 times (HBM-counter calibration)")
     a = ap.parse_args()
+    DIM = a.head_dim
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (the attention path has no multi-GPU part); got --gpus {a.gpus}",
               file=sys.stderr)
@@ -264,7 +269,7 @@ def main() -> int:
     kernel_ms = sum(durations) / len(durations)  # average launch duration
     achieved = fwd_flops / len(durations) / (kernel_ms * 1e-3) / 1e12
     traffic = None
-    if seqs == SEQS and not a.causal:
+    if seqs == SEQS and not a.causal and DIM == 64:
         traffic = measured_traffic()
     # Per shape: the table entry the forward runs, its average launch time and roofline fraction.
     from tattn import _lib
@@ -285,7 +290,7 @@ def main() -> int:
     names = sorted({entry_name(n) for n in seqs})
     roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                 "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic,
-                "kernel": f"tattn::{' / '.join(names)} (fp16, D=64, {'causal' if a.causal else 'non-causal'})",
+                "kernel": f"tattn::{' / '.join(names)} (fp16, D={DIM}, {'causal' if a.causal else 'non-causal'})",
                 "avg_launch_ms": kernel_ms, "launches": len(durations),
                 "flops_per_launch": fwd_flops / len(durations), "per_n": per_n}
 
@@ -347,7 +352,7 @@ def main() -> int:
         "dtype": "fp16",
         "data": "synthetic N(0,1), device generator seeded with N",
         "config": {
-            "workload": f"attention {head_mode}, fp16, {'causal' if a.causal else 'non-causal'}, H=16, D=64, "
+            "workload": f"attention {head_mode}, fp16, {'causal' if a.causal else 'non-causal'}, H=16, D={DIM}, "
                         f"one pass over each of N={','.join(map(str, seqs))} with B=16384/N",
             "tokens_per_shape": TOKENS, "heads": HEADS, "head_dim": DIM, "seqs": list(seqs),
         },

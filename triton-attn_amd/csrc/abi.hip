@@ -108,9 +108,10 @@ int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N, int64_t
   switch (kernel) {
     case TATTN_K_FWD:  // persistent where it fits (D=64); else 128-row blocks short, 256 / 512 long
       if (D == 64) {
-        // Persistent 4 x 1 (causal) and 4 x 2 (non-causal), ring of 4: fastest at every benchmark
-        // length (cold-cache medians, 16,384 tokens x 16 heads).
-        const int pid = causal ? 5 : 7;
+        // Persistent, ring of 4: 4 x 2 non-causal, and causal from N = 4096 (one pair of blocks per
+        // workgroup, time-sliced priority); 4 x 1 causal below. Fastest at every benchmark length
+        // (cold-cache medians, 16,384 tokens x 16 heads).
+        const int pid = causal && N < 4096 ? 5 : 7;
         if (fwd_persist_fits(FwdTable<_Float16, 64>::e[pid], ZH, N, causal != 0)) return pid;
       }
       if (D == 128) return 0;

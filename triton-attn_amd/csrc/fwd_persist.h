@@ -393,8 +393,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_persist_kernel(const FwdPara
   // the second crawls, and ends alone on its last item, at the lower throughput of one
   // workgroup per CU.
   const int rank = blockIdx.x / p.cus;
+  // A workgroup with a single work item (causal entries with 256-row blocks: one pair of blocks
+  // per slot) would keep one priority for its whole life; it switches on a global time slice of
+  // 4096 ticks of the 100 MHz counter (41 us) instead, out of phase by rank.
+  const bool time_prio = n_items == 1;
   for (int t = 0; t < nseg; ++t) {
-    if (t % SPI == 0) {
+    if (t % SPI == 0 && !time_prio) {
       if (((t / SPI) + rank) & 1) __builtin_amdgcn_s_setprio(1);
       else __builtin_amdgcn_s_setprio(0);
     }
@@ -444,6 +448,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_persist_kernel(const FwdPara
     // R consecutive steps from i (i % R == 0); the S / P register sets alternate.
     auto group = [&](int i, auto last_tag, int ii0) __attribute__((always_inline)) {
       auto ii = [&](int k) __attribute__((always_inline)) { return ii0 < 0 ? -1 : ii0 + k; };
+      if (time_prio) {
+        const uint32_t slot = (uint32_t)(__builtin_amdgcn_s_memrealtime() >> 12);
+        if ((slot + (uint32_t)rank) & 1) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+      }
       step(i, sa, sb, pa, pb, IC<0>{}, last_tag, ii(0));
       step(i + 1, sb, sa, pb, pa, IC<1>{}, last_tag, ii(1));
       step(i + 2, sa, sb, pa, pb, IC<2>{}, last_tag, ii(2));

@@ -64,7 +64,7 @@ inline bool bwd_persist_fits(const TileEntry& e, int64_t ZH, int64_t N, bool cau
 // per wave (the causal kernel with two tiles per wave needs more than the 256 registers a wave
 // has at two waves per SIMD; those entries run their pipelined twin for causal problems).
 constexpr bool fwd_persist_causal_ok(const TileEntry& e) {
-  return e.tiles == 1 && (e.nw * e.tiles) % e.ring == 0 && e.nw * e.tiles / e.ring <= 2;
+  return (e.tiles == 1 || e.ring == 4) && (e.nw * e.tiles) % e.ring == 0 && e.nw * e.tiles / e.ring <= 2;
 }
 inline bool fwd_persist_fits(const TileEntry& e, int64_t ZH, int64_t N, bool causal) {
   const int64_t bm = (int64_t)e.nw * e.tiles * 32;

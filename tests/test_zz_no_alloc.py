@@ -49,15 +49,18 @@ def _no_alloc(lib, q, k, v, o, do, m, causal, scale, code):
     return dq, dk, dv
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-def test_no_alloc_backward_gives_the_bits_of_tattn_bwd(dtype, causal):
+def test_no_alloc_backward_gives_the_bits_of_tattn_bwd(dtype, causal, d):
+    """Every call smaller than the one before. The 16-bit picks compute delta inside dQ and store
+    it in the workspace: the persistent dQ at (1, 8, 512, 64), the paired-wave dQ at head dim 128."""
     from tattn import _lib
     from tattn.api import _DTYPES, _forward
 
     lib = _lib.load()
     code = _DTYPES[dtype]
-    for i, shape in enumerate([(2, 3, 333, 64), (1, 2, 77, 64)]):  # second call smaller
+    for i, shape in enumerate([(1, 8, 512, d), (2, 3, 333, d), (1, 2, 77, d)]):
         print(f"noalloc: dtype={dtype} causal={causal} shape={shape}", flush=True)
         q, k, v, do = (rand(shape, dtype, 900 + 10 * i + s, DEV) for s in range(4))
         o, m = _forward(q, k, v, causal, 0.125)

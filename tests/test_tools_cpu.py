@@ -4,6 +4,7 @@ assembly (tattn.benchsuite, with fake implementations and a fixed timer on the C
 markdown report of tattn.report."""
 
 import json
+from pathlib import Path
 
 import pytest
 
@@ -204,6 +205,19 @@ def test_report_check_flags_broken_files(tmp_path):
     assert report.main([str(bad), "--check"]) == 1
     assert any("lacks ['status']" in p for p in report.problems(res))
     assert any("non-finite" in p for p in report.problems(res))
+
+
+def test_committed_suite_results_are_valid_and_rendered():
+    """results/gfx950.json (the suite's last run on an MI355X) has the current schema, every cell of
+    the grid and finite errors, and results/gfx950.md is its rendering."""
+    path = Path(__file__).resolve().parent.parent / "results" / "gfx950.json"
+    res = json.loads(path.read_text())
+    assert report.problems(res) == []
+    assert {(c["impl"], c["n"], c["mask"], c["pass"]) for c in res["cells"]} >= {
+        ("tattn", n, m, p) for n in (512, 1024, 2048, 4096, 8192, 16384) for m in ("none", "causal")
+        for p in ("fwd", "fwd+bwd")}
+    assert all(c["status"] == "ok" for c in res["cells"] if c["impl"] == "tattn")
+    assert path.with_suffix(".md").read_text() == report.render(res)
 
 
 @pytest.fixture(scope="module")

@@ -21,7 +21,6 @@
 
 #include <algorithm>
 
-#include "bwd_persist.h"
 #include "bwd_pipe.h"
 #include "bwd_split.h"
 #include "common.h"
@@ -615,31 +614,6 @@ struct Entry {
 // Buffer descriptors address a (z, h) slice with 32-bit offsets (plus two steps of look-ahead).
 static bool slice_fits32(const BwdParams& p, int D) { return bwd_fits32(p, D); }
 
-// Persistent dQ: grid of one workgroup per resident slot (at most), the work split per XCD into
-// whole rounds.
-template <typename T, int D, int NW, int OCC, bool CAUSAL, bool DKDV>
-static int launch_bwd_persist(BwdParams p, hipStream_t st) {
-  static_assert(!DKDV, "persistent backward: dQ only");
-  auto kern = dq_persist_kernel<T, D, NW, OCC, CAUSAL>;
-  const int nb = p.N / (NW * 32);
-  const int64_t items_x = (int64_t)p.Z * p.H / 8 * (CAUSAL ? nb / 2 : nb);
-  if (items_x >= (1 << 30)) return set_error(TATTN_E_ARG, "problem too large");
-  static int per_cu = 0;  // resident workgroups per CU (same on every gfx950)
-  if (per_cu <= 0) {
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, NW * 64, 0) != hipSuccess || n <= 0) n = 1;
-    per_cu = n;
-  }
-  p.cus = device_cus();
-  const int64_t slots_x = std::max<int64_t>(1, (int64_t)per_cu * p.cus / 8);
-  const int64_t rounds = (items_x + slots_x - 1) / slots_x;
-  p.n_blocks = nb;
-  p.items_x = (int32_t)items_x;
-  p.gx = (int32_t)((items_x + rounds - 1) / rounds);
-  kern<<<dim3(8u * (unsigned)p.gx), dim3(NW * 64), 0, st>>>(p);
-  return check_launch(DKDV ? "tattn_bwd_dkdv" : "tattn_bwd_dq");
-}
-
 template <typename T, int D, int I>
 static int launch_dkdv_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   constexpr TileEntry e = DkdvTable<T, D>::e[I];
@@ -715,9 +689,8 @@ static int launch_dq_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   } else if constexpr (e.pipe >= 1) {
     static_assert(sizeof(T) == 2 && D <= 128 && e.tiles == 1 && e.other == 32, "pipelined dQ shape");
     if constexpr (e.pipe == 2) {
-      if (slice_fits32(p, D) && bwd_persist_fits(e, (int64_t)p.Z * p.H, p.N, causal))
-        return causal ? launch_bwd_persist<T, D, e.nw, e.occ, true, false>(p0, st)
-                      : launch_bwd_persist<T, D, e.nw, e.occ, false, false>(p0, st);
+      if (slice_fits32(p, D) && bwd_persist_fits(e, (int64_t)p.Z * p.H, p.N, causal))  // own translation unit
+        return launch_dq_persist(p0, D, std::is_same_v<T, bf16> ? 2 : 0, I, causal, st);
     }
     if (slice_fits32(p, D)) {
       if (causal)

@@ -142,6 +142,10 @@ __device__ __forceinline__ float row_delta(float (&s)[NS]) {
   return sum_halves(s[0]);
 }
 
+// Forward softmax: the max used in the exponent moves only when a row's true max exceeds it by
+// more than 2^kRescaleLog2 (lazy rescaling, exact in real arithmetic).
+constexpr float kRescaleLog2 = 8.0f;
+
 // Key permutation inside a 32-row tile: swaps bits 2 and 3 of the row index. Storing key r of
 // a tile at LDS row perm32(r) makes the MFMA C layout hand every lane-half 8 consecutive keys
 // per 16-key slice: C register r of lane-half h then holds key kappa(r, h).

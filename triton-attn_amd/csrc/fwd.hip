@@ -29,8 +29,6 @@
 
 namespace tattn {
 
-constexpr float kRescaleLog2 = 8.0f;
-
 template <typename T, int D, int NW, int QT, int BN>
 struct FwdCfg {
   static constexpr int NT = NW * 64;
@@ -744,37 +742,6 @@ namespace tattn {
 
 // ---- launch ------------------------------------------------------------------------------
 
-// Persistent forward: grid of one workgroup per resident slot (at most), the work split per XCD
-// into whole rounds. Returns 1 (nothing launched) when the problem does not meet the kernel's
-// preconditions.
-template <typename T, int D, int NW, int QT, int OCC, bool CAUSAL, int R>
-static int launch_fwd_persist(FwdParams p, hipStream_t st, int* rc) {
-  constexpr int BM = NW * QT * 32;
-  constexpr TileEntry self{NW, QT, 32, OCC, 2, R};
-  const int64_t S = (int64_t)p.Z * p.H;
-  if (!fwd_persist_fits(self, S, p.N, CAUSAL)) return 1;
-  const int nb = p.N / BM;
-  const int64_t items_x = S / 8 * (CAUSAL ? nb / 2 : nb);
-  if (items_x >= (1 << 30)) return 1;
-  static int per_cu = 0;  // resident workgroups per CU (same on every gfx950)
-  if (per_cu <= 0) {
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fwd_persist_kernel<T, D, NW, QT, OCC, CAUSAL, R>, NW * 64, 0) !=
-            hipSuccess || n <= 0)
-      n = 1;
-    per_cu = n;
-  }
-  p.cus = device_cus();
-  const int64_t slots_x = std::max<int64_t>(1, (int64_t)per_cu * p.cus / 8);
-  const int64_t rounds = (items_x + slots_x - 1) / slots_x;
-  p.n_qblocks = nb;
-  p.items_x = (int32_t)items_x;
-  p.gx = (int32_t)((items_x + rounds - 1) / rounds);
-  fwd_persist_kernel<T, D, NW, QT, OCC, CAUSAL, R><<<dim3(8u * (unsigned)p.gx), dim3(NW * 64), 0, st>>>(p);
-  *rc = check_launch("tattn_fwd");
-  return 0;
-}
-
 template <typename T, int D, int I>
 static int launch_fwd_entry(const FwdParams& p0, bool causal, hipStream_t st) {
   constexpr TileEntry e = FwdTable<T, D>::e[I];
@@ -800,8 +767,11 @@ static int launch_fwd_entry(const FwdParams& p0, bool causal, hipStream_t st) {
     if constexpr (e.pipe == 2) {  // persistent, where the problem fits it
       int rc = TATTN_OK;
       if (causal) {
-        if constexpr (fwd_persist_causal_ok(e))
+        if constexpr (fwd_persist_causal_ok(e) && e.tiles == 2) {  // own translation unit
+          if (launch_fwd_persist_causal2(p0, D, std::is_same_v<T, bf16> ? 2 : 0, I, st, &rc) == 0) return rc;
+        } else if constexpr (fwd_persist_causal_ok(e)) {
           if (launch_fwd_persist<T, D, e.nw, e.tiles, e.occ, true, e.ring>(p0, st, &rc) == 0) return rc;
+        }
       } else if (launch_fwd_persist<T, D, e.nw, e.tiles, e.occ, false, e.ring>(p0, st, &rc) == 0) {
         return rc;
       }

@@ -36,6 +36,13 @@
 // steps) one or two ring periods, 32-bit slice offsets.
 #pragma once
 
+#include <algorithm>
+#include <type_traits>
+
+#include "common.h"
+#include "launch.h"
+#include "tiles.h"
+
 namespace tattn {
 
 // LDS of the persistent forward: R K slots and R V slots of 32 unpadded rows.
@@ -517,6 +524,37 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_persist_kernel(const FwdPara
   }
   // No LDS DMA may still be in flight when the workgroup's LDS is released.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+}
+
+// Persistent forward: grid of one workgroup per resident slot (at most), the work split per XCD
+// into whole rounds. Returns 1 (nothing launched) when the problem does not meet the kernel's
+// preconditions.
+template <typename T, int D, int NW, int QT, int OCC, bool CAUSAL, int R>
+int launch_fwd_persist(FwdParams p, hipStream_t st, int* rc) {
+  constexpr int BM = NW * QT * 32;
+  constexpr TileEntry self{NW, QT, 32, OCC, 2, R};
+  const int64_t S = (int64_t)p.Z * p.H;
+  if (!fwd_persist_fits(self, S, p.N, CAUSAL)) return 1;
+  const int nb = p.N / BM;
+  const int64_t items_x = S / 8 * (CAUSAL ? nb / 2 : nb);
+  if (items_x >= (1 << 30)) return 1;
+  static int per_cu = 0;  // resident workgroups per CU (same on every gfx950)
+  if (per_cu <= 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fwd_persist_kernel<T, D, NW, QT, OCC, CAUSAL, R>, NW * 64, 0) !=
+            hipSuccess || n <= 0)
+      n = 1;
+    per_cu = n;
+  }
+  p.cus = device_cus();
+  const int64_t slots_x = std::max<int64_t>(1, (int64_t)per_cu * p.cus / 8);
+  const int64_t rounds = (items_x + slots_x - 1) / slots_x;
+  p.n_qblocks = nb;
+  p.items_x = (int32_t)items_x;
+  p.gx = (int32_t)((items_x + rounds - 1) / rounds);
+  fwd_persist_kernel<T, D, NW, QT, OCC, CAUSAL, R><<<dim3(8u * (unsigned)p.gx), dim3(NW * 64), 0, st>>>(p);
+  *rc = check_launch("tattn_fwd");
+  return 0;
 }
 
 }  // namespace tattn

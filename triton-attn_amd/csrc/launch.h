@@ -29,6 +29,16 @@ int launch_bwd_dq(const BwdParams& p, int D, int dtype, bool causal, int config_
 
 int fwd_lds_bytes(int D, int dtype, const TileEntry& e);
 
+// Kernels that get their own translation unit, compiled with the instruction scheduler that
+// measured fastest for them (tattn/_build.py: SOURCE_FLAGS); dtype 0 = fp16, 2 = bf16.
+// Persistent causal forward with two query tiles per wave (fwd_persist_causal.hip): runs entry
+// `config_id` of the forward table; returns 1 (nothing launched) when the problem does not fit
+// the kernel, else 0 with *rc the launch status.
+int launch_fwd_persist_causal2(const FwdParams& p, int D, int dtype, int config_id, hipStream_t st, int* rc);
+// Persistent dQ (bwd_dq_persist.hip): runs entry `config_id` of the dQ table; the caller has
+// checked bwd_persist_fits and bwd_fits32.
+int launch_dq_persist(const BwdParams& p, int D, int dtype, int config_id, bool causal, hipStream_t st);
+
 // Whether the backward's (z, h) slices fit 32-bit buffer offsets (plus two steps of look-ahead):
 // the pipelined and persistent backward kernels need it, the generic ones take 64-bit addresses.
 inline bool bwd_fits32(const BwdParams& p, int D) {

@@ -18,10 +18,17 @@ CSRC = PKG.parent / "csrc"
 REPO = PKG.parent.parent
 INCLUDE = REPO / "include"
 LIB = PKG / "libtattn_hip.so"
-SOURCES = ["abi.hip", "fwd.hip", "bwd.hip"]
+SOURCES = ["abi.hip", "fwd.hip", "fwd_persist_causal.hip", "bwd.hip", "bwd_dq_persist.hip"]
 # Per-source flags. fwd.hip: keep each step's softmax work in the step that issues the
 # independent MFMAs it interleaves with (machine sinking would move it to its first use).
-SOURCE_FLAGS = {"fwd.hip": ["-mllvm", "-disable-machine-sink"]}
+# fwd_persist_causal.hip (persistent causal forward, two tiles per wave) and bwd_dq_persist.hip
+# (persistent dQ) hold one kernel family each so that they can take the LLVM instruction
+# scheduler that measured fastest for them; the other kernels are slower under either.
+SOURCE_FLAGS = {
+    "fwd.hip": ["-mllvm", "-disable-machine-sink"],
+    "fwd_persist_causal.hip": ["-mllvm", "-disable-machine-sink", "-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+    "bwd_dq_persist.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+}
 ARCH = "gfx950"
 
 

@@ -228,7 +228,7 @@ def bwd_asm():
 @pytest.fixture(scope="module")
 def own_scheduler_asm():
     """The translation units built with their own instruction scheduler."""
-    return [diagnose.compile_asm(diagnose.CSRC / s) for s in ("fwd_persist_causal.hip", "bwd_dq_persist.hip")]
+    return [diagnose.compile_asm(diagnose.CSRC / s) for s in ("fwd_persist_causal.hip", "bwd_dq_persist.hip", "bwd_split.hip")]
 
 
 @pytest.mark.skipif(not _have_hipcc(), reason="hipcc not installed")
@@ -260,6 +260,7 @@ def test_each_kernel_lives_in_one_translation_unit(fwd_asm, bwd_asm, own_schedul
         seen.update(set(re.findall(r"^\s*\.amdhsa_kernel (\S+)", asm, re.M)))
     dups = [k for k, n in seen.items() if n > 1]
     assert not dups, dups
-    causal2, dq_persist = (set(re.findall(r"^\s*\.amdhsa_kernel (\S+)", a, re.M)) for a in own_scheduler_asm)
+    causal2, dq_persist, split = (set(re.findall(r"^\s*\.amdhsa_kernel (\S+)", a, re.M)) for a in own_scheduler_asm)
     assert causal2 and all("fwd_persist_kernel" in k for k in causal2)
     assert dq_persist and all("dq_persist_kernel" in k for k in dq_persist)
+    assert split and all("_split_kernel" in k for k in split)

@@ -22,7 +22,6 @@
 #include <algorithm>
 
 #include "bwd_pipe.h"
-#include "bwd_split.h"
 #include "common.h"
 #include "launch.h"
 #include "tiles.h"
@@ -623,15 +622,9 @@ static int launch_dkdv_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   const int64_t blocks = (int64_t)p.n_blocks * p.Z * p.H;
   if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(e.nw * 64);
-  if constexpr (e.pipe == 3) {  // paired waves, 128 keys per workgroup
+  if constexpr (e.pipe == 3) {  // paired waves, 128 keys per workgroup (own translation unit)
     static_assert(sizeof(T) == 2 && e.nw == 8 && e.tiles == 1 && e.other == 32, "paired-wave dK/dV shape");
-    if (slice_fits32(p, D)) {
-      if (causal)
-        dkdv_split_kernel<T, D, true><<<grid, block, 0, st>>>(p);
-      else
-        dkdv_split_kernel<T, D, false><<<grid, block, 0, st>>>(p);
-      return check_launch("tattn_bwd_dkdv");
-    }
+    if (slice_fits32(p, D)) return launch_split(p, D, std::is_same_v<T, bf16> ? 2 : 0, true, causal, st);
     p.n_blocks = (p.N + 127) / 128;  // slices beyond 2 GiB: 64-bit addressing
     const dim3 g2((unsigned)((int64_t)p.n_blocks * p.Z * p.H));
     if (causal)
@@ -671,15 +664,9 @@ static int launch_dq_entry(const BwdParams& p0, bool causal, hipStream_t st) {
   const int64_t blocks = (int64_t)p.n_blocks * p.Z * p.H;
   if (blocks > 0x7fffffff) return set_error(TATTN_E_ARG, "grid too large: %lld workgroups", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(e.nw * 64);
-  if constexpr (e.pipe == 3) {  // paired waves, 128 queries per workgroup
+  if constexpr (e.pipe == 3) {  // paired waves, 128 queries per workgroup (own translation unit)
     static_assert(sizeof(T) == 2 && e.nw == 8 && e.tiles == 1 && e.other == 32, "paired-wave dQ shape");
-    if (slice_fits32(p, D)) {
-      if (causal)
-        dq_split_kernel<T, D, true><<<grid, block, 0, st>>>(p);
-      else
-        dq_split_kernel<T, D, false><<<grid, block, 0, st>>>(p);
-      return check_launch("tattn_bwd_dq");
-    }
+    if (slice_fits32(p, D)) return launch_split(p, D, std::is_same_v<T, bf16> ? 2 : 0, false, causal, st);
     p.n_blocks = (p.N + 127) / 128;  // slices beyond 2 GiB: 64-bit addressing
     const dim3 g2((unsigned)((int64_t)p.n_blocks * p.Z * p.H));
     if (causal)

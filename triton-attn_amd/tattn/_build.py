@@ -18,16 +18,18 @@ CSRC = PKG.parent / "csrc"
 REPO = PKG.parent.parent
 INCLUDE = REPO / "include"
 LIB = PKG / "libtattn_hip.so"
-SOURCES = ["abi.hip", "fwd.hip", "fwd_persist_causal.hip", "bwd.hip", "bwd_dq_persist.hip"]
+SOURCES = ["abi.hip", "fwd.hip", "fwd_persist_causal.hip", "bwd.hip", "bwd_dq_persist.hip", "bwd_split.hip"]
 # Per-source flags. fwd.hip: keep each step's softmax work in the step that issues the
 # independent MFMAs it interleaves with (machine sinking would move it to its first use).
-# fwd_persist_causal.hip (persistent causal forward, two tiles per wave) and bwd_dq_persist.hip
-# (persistent dQ) hold one kernel family each so that they can take the LLVM instruction
-# scheduler that measured fastest for them; the other kernels are slower under either.
+# fwd_persist_causal.hip (persistent causal forward, two tiles per wave), bwd_dq_persist.hip
+# (persistent dQ) and bwd_split.hip (paired-wave dK/dV and dQ) hold one kernel family each so
+# that they can take the LLVM instruction scheduler that measured fastest for them; the other
+# kernels are slower under either.
 SOURCE_FLAGS = {
     "fwd.hip": ["-mllvm", "-disable-machine-sink"],
     "fwd_persist_causal.hip": ["-mllvm", "-disable-machine-sink", "-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "bwd_dq_persist.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "bwd_split.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
 }
 ARCH = "gfx950"
 

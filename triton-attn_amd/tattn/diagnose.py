@@ -4,7 +4,7 @@ The counterpart of the reference's bench/diagnose.py:1-80, which counts `mma.syn
 and fp32 `fma` in the PTX Triton emits. Here the evidence is our own gfx950 assembly (code built
 in this repository, read as text) and rocprofv3 counter output:
 
-    python -m tattn.diagnose [--sources fwd.hip,fwd_persist_causal.hip,bwd.hip,bwd_dq_persist.hip] [--kernel SUBSTR] [--out FILE]
+    python -m tattn.diagnose [--sources fwd.hip,fwd_persist_causal.hip,bwd.hip,bwd_dq_persist.hip,bwd_split.hip] [--kernel SUBSTR] [--out FILE]
     python -m tattn.diagnose --counters DIR [DIR ...]
 
 ISA mode compiles the library's kernel sources to assembly with the build's flags and reports,
@@ -234,7 +234,7 @@ def derived(cs: dict[str, float]) -> dict[str, float]:
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--sources", default="fwd.hip,fwd_persist_causal.hip,bwd.hip,bwd_dq_persist.hip", help="kernel sources under csrc/")
+    ap.add_argument("--sources", default="fwd.hip,fwd_persist_causal.hip,bwd.hip,bwd_dq_persist.hip,bwd_split.hip", help="kernel sources under csrc/")
     ap.add_argument("--kernel", default="pipe_kernel", help="substring of the mangled kernel names")
     ap.add_argument("--counters", nargs="*", help="rocprofv3 --pmc output directories (counter mode)")
     ap.add_argument("--out", default=None, help="write the JSON result here")

@@ -29,19 +29,19 @@ def _gpu():
 
 
 def _persistent_entries():
+    """(head dim, persistent entry, pipelined entry of the same tiles) for every kind-2 forward entry."""
     if not torch.cuda.is_available():
         return []
     from tattn import _lib
 
     out = []
-    for c in range(_lib.num_configs(_lib.K_FWD, 64, _lib.F16)):
-        desc = _lib.config_desc(_lib.K_FWD, 64, _lib.F16, c)
-        if desc["kind"] == 2:
-            twin = next(t for t in range(_lib.num_configs(_lib.K_FWD, 64, _lib.F16))
-                        if _lib.config_desc(_lib.K_FWD, 64, _lib.F16, t)["kind"] == 1
-                        and (_lib.config_desc(_lib.K_FWD, 64, _lib.F16, t)["waves"],
-                             _lib.config_desc(_lib.K_FWD, 64, _lib.F16, t)["tiles"]) == (desc["waves"], desc["tiles"]))
-            out.append((c, twin))
+    for d in (16, 32, 64, 128):
+        descs = [_lib.config_desc(_lib.K_FWD, d, _lib.F16, c) for c in range(_lib.num_configs(_lib.K_FWD, d, _lib.F16))]
+        for c, desc in enumerate(descs):
+            if desc["kind"] == 2:
+                twin = next(t for t, o in enumerate(descs)
+                            if o["kind"] == 1 and (o["waves"], o["tiles"]) == (desc["waves"], desc["tiles"]))
+                out.append((d, c, twin))
     return out
 
 
@@ -59,25 +59,26 @@ def _reference(q, k, v, causal, scale):
     return torch.cat(o, 1), torch.cat(m, 1)
 
 
-@pytest.mark.parametrize("entry", _persistent_entries(), ids=lambda e: f"cfg{e[0]}")
+@pytest.mark.parametrize("entry", _persistent_entries(), ids=lambda e: f"d{e[0]}cfg{e[1]}")
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_persistent_forward(entry, shape, causal, dtype):
     from tattn.api import _forward
 
-    cid, twin = entry
+    d, cid, twin = entry
     b, h, n = shape
-    print(f"persistent fwd: cfg{cid} shape={shape} causal={causal} {dtype}", flush=True)
+    scale = d ** -0.5
+    print(f"persistent fwd: d={d} cfg{cid} shape={shape} causal={causal} {dtype}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(n * 7 + b + int(causal))
-    q, k, v = (torch.randn(b, h, n, 64, device=DEV, dtype=dtype, generator=g) for _ in range(3))
-    o, m = _forward(q, k, v, causal, 0.125, config=cid)
-    o2, m2 = _forward(q, k, v, causal, 0.125, config=twin)
+    q, k, v = (torch.randn(b, h, n, d, device=DEV, dtype=dtype, generator=g) for _ in range(3))
+    o, m = _forward(q, k, v, causal, scale, config=cid)
+    o2, m2 = _forward(q, k, v, causal, scale, config=twin)
     torch.cuda.synchronize()
-    want_o, want_m = _reference(q, k, v, causal, 0.125)
+    want_o, want_m = _reference(q, k, v, causal, scale)
     bound = F16_MAX if dtype == torch.float16 else 8 * F16_MAX
-    check_max(f"cfg{cid} {shape} causal={causal} {dtype} o", o, want_o, bound)
-    check_max(f"cfg{cid} {shape} causal={causal} {dtype} M", m, want_m, 1e-3 if dtype == torch.float16 else 8e-3)
+    check_max(f"d{d} cfg{cid} {shape} causal={causal} {dtype} o", o, want_o, bound)
+    check_max(f"d{d} cfg{cid} {shape} causal={causal} {dtype} M", m, want_m, 1e-3 if dtype == torch.float16 else 8e-3)
     # Same math as the pipelined kernel: equal up to the rounding of the softmax's lazy max moves.
     torch.testing.assert_close(o.float(), o2.float(), atol=2 ** -10, rtol=2 ** -9)
     torch.testing.assert_close(m, m2, atol=1e-4, rtol=0)
@@ -87,13 +88,14 @@ def test_persistent_inference_path_and_repeat():
     """M = NULL (inference) gives the same O; two calls in a row give the same bits."""
     from tattn.api import _forward
 
-    cid = _persistent_entries()[0][0]
-    q, k, v = (torch.randn(4, 16, 1024, 64, device=DEV, dtype=torch.float16) for _ in range(3))
-    for causal in (False, True):
-        o1, _ = _forward(q, k, v, causal, 0.125, config=cid)
-        o2, m2 = _forward(q, k, v, causal, 0.125, config=cid, save_lse=False)
-        o3, _ = _forward(q, k, v, causal, 0.125, config=cid)
-        assert m2 is None and torch.equal(o1, o2) and torch.equal(o1, o3)
+    for d in (64, 128):
+        cid = next(c for dd, c, _ in _persistent_entries() if dd == d)
+        q, k, v = (torch.randn(4, 16, 1024, d, device=DEV, dtype=torch.float16) for _ in range(3))
+        for causal in (False, True):
+            o1, _ = _forward(q, k, v, causal, d ** -0.5, config=cid)
+            o2, m2 = _forward(q, k, v, causal, d ** -0.5, config=cid, save_lse=False)
+            o3, _ = _forward(q, k, v, causal, d ** -0.5, config=cid)
+            assert m2 is None and torch.equal(o1, o2) and torch.equal(o1, o3)
 
 
 def _bwd_entries(kernel):

@@ -106,7 +106,7 @@ const TileEntry* config_entry(int kernel, int64_t D, int dtype, int id) {
 int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N, int64_t ZH) {
   if (dtype == TATTN_F32) return 0;  // fp16 and bf16 share the picks
   switch (kernel) {
-    case TATTN_K_FWD:  // persistent where it fits (D=64); else 128-row blocks short, 256 / 512 long
+    case TATTN_K_FWD:  // persistent where it fits (D=64, 128); else 128-row blocks short, 256 / 512 long
       if (D == 64) {
         // Persistent, ring of 4: 4 x 2 non-causal, and causal from N = 4096 (one pair of blocks per
         // workgroup, time-sliced priority); 4 x 1 causal below. Fastest at every benchmark length
@@ -114,7 +114,13 @@ int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N, int64_t
         const int pid = causal && N < 4096 ? 5 : 7;
         if (fwd_persist_fits(FwdTable<_Float16, 64>::e[pid], ZH, N, causal != 0)) return pid;
       }
-      if (D == 128) return 0;
+      if (D == 128) {
+        // Persistent, ring of 4: 8 x 1 from N = 2048 (causal: 4096), 4 x 1 below; else 4 x 1
+        // pipelined.
+        const int pid = N >= (causal ? 4096 : 2048) ? 3 : 2;
+        if (fwd_persist_fits(FwdTable<_Float16, 128>::e[pid], ZH, N, causal != 0)) return pid;
+        return 0;
+      }
       if (causal) return N >= 4096 ? 0 : 1;
       if (D == 64) return N >= 4096 ? 3 : N >= 1024 ? 0 : 1;
       return D == 16 && N < 2048 ? 1 : 0;

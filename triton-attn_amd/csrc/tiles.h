@@ -41,16 +41,18 @@ template <typename T, int D> struct FwdTable;
   TATTN_TABLE(NAME, __bf16, D, __VA_ARGS__)
 
 // The picks per sequence length are measured and live in pick_config (abi.hip); entry 0 is the
-// pick wherever no rule names another. 16-bit forward entries and the 16-bit backward
-// entries marked pipe run the software-pipelined kernels (32 rows per step). Every 16-bit
-// entry fits its register budget without scratch and can reach its waves per SIMD within the
-// 160 KB of LDS (a D=64 forward workgroup holds 44 KB of K/V ring); D=128 entries run at one
-// wave per SIMD (512 registers). Of the fp32 kernels only causal dK/dV at D=128 spills (32 bytes).
+// pick wherever no rule names another. Kinds (`pipe`): 1 software-pipelined (32 rows per step),
+// 2 persistent (16-bit; where a problem does not meet its preconditions the pipelined kernel of
+// the same tiles runs it), 3 paired-wave backward, 0 generic. The 16-bit entries fit their
+// register budgets (512 / waves per SIMD) without scratch, except the causal persistent forward
+// with two tiles per wave (96 bytes), and reach their waves per SIMD within the 160 KB of LDS (a
+// persistent forward workgroup holds a 32 KB K/V ring at D=64, 64 KB at D=128). Of the fp32
+// kernels only causal dK/dV at D=128 spills (32 bytes).
 TATTN_TABLE16(FwdTable, 16, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1})
 TATTN_TABLE16(FwdTable, 32, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1})
 TATTN_TABLE16(FwdTable, 64, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {8, 2, 32, 2, 1},
               {4, 2, 32, 2, 2, 8}, {4, 1, 32, 2, 2, 4}, {8, 1, 32, 2, 2, 8}, {4, 2, 32, 2, 2, 4})
-TATTN_TABLE16(FwdTable, 128, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1})
+TATTN_TABLE16(FwdTable, 128, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 32, 2, 2, 4}, {8, 1, 32, 2, 2, 4})
 TATTN_TABLE(FwdTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(FwdTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(FwdTable, float, 64, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})

@@ -11,10 +11,15 @@ step's counted flops divided by its time. The same line carries the roofline of 
 kernel (HIP events around every forward launch of the timed steps, on the launch stream), the
 per-N sweep (forward, causal and non-causal; fwd+bwd, causal and non-causal, with peak extra
 memory) timed like the reference's tables (tattn.timing.do_bench: cache flushed before each
-call, median over ~100 ms), the accuracy of each shape as the reference's benchmark measures it
-(bench/bench.py:128-171: forward max / mean abs error against float32 attention at every N and
-both masks, dq/dk/dv max abs error against float32 autograd at N = 1024 and 4096), and a CPU
-baseline: the oracle's tiled forward timed on the host cores on a bounded sample.
+call, median over ~100 ms), the roofline of the two backward kernels per N and mask
+(`roofline.bwd`: dK/dV and dQ each timed alone through the C ABI, and tattn_bwd whole), a
+measured HBM yardstick (`roofline.hbm_copy_tbps`: a 256 MiB device copy, the memory analog of
+the reference's GEMM yardstick, bench/bench.py:173-175), the accuracy of each shape as the
+reference's benchmark measures it (bench/bench.py:128-171: forward max / mean abs error against
+float32 attention at every N and both masks, dq/dk/dv max abs error against float32 autograd at
+N = 1024 and 4096, batch 0) plus causal gradients over the whole N = 512 tensors beside the
+error of the reference's own algorithm on them, and a CPU baseline: the oracle's tiled forward
+timed on the host cores on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline] [--no-accuracy]
        (profiling: --no-sweep --seqs N --causal --backward --head-dim D)
@@ -161,7 +166,130 @@ def accuracy(data) -> list[dict]:
             for name, got, want in (("dq", qg.grad, qr.grad), ("dk", kg.grad, kr.grad), ("dv", vg.grad, vr.grad)):
                 rows.append({"seq": n, "causal": causal, "what": name,
                              "max_abs_err": float(f"{(got.float() - want).abs().max().item():.4g}")})
+    rows += full_tensor_causal_grads(data, 512)
     return rows
+
+
+def full_tensor_causal_grads(data, n: int) -> list[dict]:
+    """Causal dq, dk, dv over the whole [B, 16, N, 64] tensors (all batches and heads) against float32
+    autograd, with beside each the error of the reference's own backward algorithm with its
+    kernels' rounding points (oracle.reference.rounded_backward) on the same inputs (q, k, v, dO
+    and the forward's O and M), and of the reference's whole pipeline (the same algorithm from the
+    exact log-sum-exp). The bound is max(2e-3, the algorithm's error + 5e-4)."""
+    import torch
+
+    from oracle.reference import naive_attention, rounded_backward
+    from tattn import attention
+    from tattn.api import _forward
+
+    _, q, k, v, do = data[n]
+    qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+    attention(qg, kg, vg, causal=True).backward(do)
+    got = (qg.grad, kg.grad, vg.grad)
+    o, m = _forward(q, k, v, True, 1.0 / math.sqrt(DIM))
+    emulated = rounded_backward(q, k, v, do, causal=True, o=o, lse=m)
+    pipeline = rounded_backward(q, k, v, do, causal=True)
+    err, emu, pipe = [0.0] * 3, [0.0] * 3, [0.0] * 3
+    per = max(1, (1 << 28) // (q.shape[1] * n * n))  # batches per chunk: ~1 GiB of scores
+    for b0 in range(0, q.shape[0], per):
+        sl = slice(b0, b0 + per)
+        qr, kr, vr = (t[sl].float().requires_grad_() for t in (q, k, v))
+        naive_attention(qr, kr, vr, causal=True).backward(do[sl].float())
+        for i, want in enumerate((qr.grad, kr.grad, vr.grad)):
+            err[i] = max(err[i], (got[i][sl].float() - want).abs().max().item())
+            emu[i] = max(emu[i], (emulated[i][sl].float() - want).abs().max().item())
+            pipe[i] = max(pipe[i], (pipeline[i][sl].float() - want).abs().max().item())
+        del qr, kr, vr
+    return [{"seq": n, "causal": True, "what": name, "scope": "all batches and heads",
+             "max_abs_err": float(f"{e:.4g}"), "reference_algorithm_max_abs_err": float(f"{r:.4g}"),
+             "reference_pipeline_max_abs_err": float(f"{pp:.4g}"),
+             "bound": float(f"{max(2e-3, r + 5e-4):.4g}")}
+            for name, e, r, pp in zip(("dq", "dk", "dv"), err, emu, pipe)]
+
+
+def backward_roofline(data, causal_modes=(False, True)) -> dict:
+    """The two backward kernels of the default path, each timed on its own with the reference's
+    timer (tattn.timing.do_bench: HIP events on the launch stream, 256 MB cache flush before each
+    call, median) through the C ABI with the library's picks: dK/dV (tattn_bwd_dkdv) and dQ
+    (tattn_bwd_dq, reading the preprocess's delta), plus tattn_bwd as one call (dQ computing delta
+    itself, then dK/dV). Executed matrix-core work per launch: dK/dV 4 GEMMs per 32 x 32 block
+    (S, dP, dV, dK) = 2 x the forward's flops, dQ 3 (S, dP, dQ) = 1.5 x; the reference's
+    convention counts the backward as 2.5 x the forward (bench/bench.py:31-35)."""
+    import torch
+
+    from tattn import _lib
+    from tattn.api import _forward
+    from tattn.timing import do_bench
+
+    lib = _lib.load()
+    scale = 1.0 / math.sqrt(DIM)
+    rows = []
+    for causal in causal_modes:
+        for n in SEQS:
+            b, q, k, v, do = data[n]
+            o, m = _forward(q, k, v, causal, scale)
+            st = _lib.strides4(q)
+            stream = torch.cuda.current_stream().cuda_stream
+            delta = torch.empty((b, HEADS, n), device=q.device, dtype=torch.float32)
+            dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+            shape = (b, HEADS, n, DIM, _lib.F16, int(causal), scale, -1, stream)
+            _lib.check(lib.tattn_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta.data_ptr(), st, b, HEADS, n, DIM,
+                                                _lib.F16, stream), "tattn_bwd_preprocess")
+
+            def dkdv() -> None:
+                lib.tattn_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), dk.data_ptr(),
+                                   dv.data_ptr(), m.data_ptr(), delta.data_ptr(), st, *shape)
+
+            def dqk() -> None:
+                lib.tattn_bwd_dq(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), dq.data_ptr(),
+                                 m.data_ptr(), delta.data_ptr(), st, *shape)
+
+            def whole() -> None:
+                lib.tattn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), dq.data_ptr(),
+                              dk.data_ptr(), dv.data_ptr(), m.data_ptr(), delta.data_ptr(), st, *shape)
+
+            f = flops(b, HEADS, n, DIM, causal, "fwd")
+            t_kv, t_q, t_all = do_bench(dkdv), do_bench(dqk), do_bench(whole)
+            row = {"seq": n, "batch": b, "causal": causal}
+            for name, ms, work in (("dkdv", t_kv, 2.0 * f), ("dq", t_q, 1.5 * f)):
+                tf = work / (ms * 1e-3) / 1e12
+                row[name] = {"entry": _lib.pick_config(_lib.K_BWD_DKDV if name == "dkdv" else _lib.K_BWD_DQ,
+                                                       DIM, _lib.F16, causal, n),
+                             "us": round(1e3 * ms, 2), "exec_tflops": round(tf, 1),
+                             "frac": round(tf / PEAK_F16_TFLOPS, 4)}
+            counted = 2.5 * f / (t_all * 1e-3) / 1e12
+            row["tattn_bwd"] = {"us": round(1e3 * t_all, 2), "counted_tflops": round(counted, 1),
+                                "frac": round(counted / PEAK_F16_TFLOPS, 4)}
+            rows.append(row)
+            print(json.dumps({"bwd_roofline": row}), file=sys.stderr, flush=True)
+            del o, m, delta, dq, dk, dv
+    return {"bound": "mfma", "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+            "timer": "cold-cache median per call (tattn.timing.do_bench), HIP events on the launch stream",
+            "work": "dkdv: 2x forward flops, dq: 1.5x (executed GEMMs); tattn_bwd: 2.5x (the reference's count)",
+            "per_n": rows}
+
+
+def hbm_copy_tbps(mib: int = 256) -> dict:
+    """Measured HBM bandwidth yardstick: a device-to-device copy of `mib` MiB (torch's copy kernel),
+    HIP events, median of 20 after 3 warm-ups; bytes moved = read + write."""
+    import torch
+
+    src = torch.empty(mib * 2**18, device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    times = []
+    for _ in range(20):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dst.copy_(src)
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1))
+    ms = statistics.median(times)
+    del src, dst
+    return {"mib": mib, "us": round(1e3 * ms, 2), "tbps": round(2 * mib * 2**20 / (ms * 1e-3) / 1e12, 3),
+            "peak_tbps": 8.0}
 
 
 def main() -> int:
@@ -294,6 +422,11 @@ def main() -> int:
                 "avg_launch_ms": kernel_ms, "launches": len(durations),
                 "flops_per_launch": fwd_flops / len(durations), "per_n": per_n}
 
+    if not a.no_sweep and seqs == SEQS and DIM == 64:
+        roofline["bwd"] = backward_roofline(data)
+        roofline["hbm_copy"] = hbm_copy_tbps(256)
+        roofline["hbm_copy_tbps"] = roofline["hbm_copy"]["tbps"]
+
     # ---- sweep: per N, forward and fwd+bwd, causal and non-causal -------------------------
     sweep = []
     agg = {}
@@ -363,11 +496,16 @@ def main() -> int:
     }
     if not a.no_accuracy and not a.no_sweep:
         out["accuracy"] = accuracy(data)
+        recipe = [r for r in out["accuracy"] if "scope" not in r]
+        full = [r for r in out["accuracy"] if "scope" in r]
         out["accuracy_worst"] = {
-            "fwd_max_abs_err": max(r["max_abs_err"] for r in out["accuracy"] if r["what"] == "o"),
-            "fwd_mean_abs_err": max(r["mean_abs_err"] for r in out["accuracy"] if r["what"] == "o"),
-            "grad_max_abs_err": max(r["max_abs_err"] for r in out["accuracy"] if r["what"] != "o"),
+            "fwd_max_abs_err": max(r["max_abs_err"] for r in recipe if r["what"] == "o"),
+            "fwd_mean_abs_err": max(r["mean_abs_err"] for r in recipe if r["what"] == "o"),
+            "grad_max_abs_err": max(r["max_abs_err"] for r in recipe if r["what"] != "o"),
             "envelope": 2e-3,
+            "full_tensor_causal_grad_max_abs_err": max(r["max_abs_err"] for r in full),
+            "full_tensor_causal_reference_algorithm": max(r["reference_algorithm_max_abs_err"] for r in full),
+            "full_tensor_causal_within_bound": all(r["max_abs_err"] <= r["bound"] for r in full),
         }
     if not a.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()

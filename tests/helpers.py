@@ -36,13 +36,18 @@ def gpu_ready() -> bool:
 # attention and its autograd.
 F16_MAX = 2e-3
 F32_MAX = 1e-5
-# fp16 gradients of causal attention on the full benchmark tensors exceed F16_MAX in any
-# implementation with the reference's rounding points: causal rows see few keys, so |dv| and
-# |dq| reach 4-8, where storing the result in fp16 alone costs up to half an ulp = 1.95e-3, on
-# top of the fp16 rounding of P and dS. The reference algorithm computed exactly in float32 with
-# those rounding points and the exact log-sum-exp reaches 3.5e-3 on these inputs (measured on
-# the MI355X: 65,536 heads of 24 tokens; 2.8e-3 at N=512). Those checks take this flat cap.
-F16_CAUSAL_GRAD_MAX = 4e-3
+# Gradients in 16 bits are held to max(envelope, E + margin), where E is the max abs error, against
+# the same float32 reference, of the reference's own backward algorithm with its rounding points
+# (oracle.reference.rounded_backward) run on the backward's inputs: q, k, v, dO and the forward's
+# saved O and M. Where that algorithm stays within the envelope the flat envelope holds; where it
+# does not (causal rows that see few keys reach |grad| of 4-8, where the 16-bit store alone costs up
+# to half an ulp), the kernel may exceed the algorithm's own error by the margin only. The margin
+# covers one last-place flip at the store: kernel and algorithm sum in different orders, so a value
+# near a rounding midpoint can land on the other neighbour, moving the error by at most the
+# distance of the exact value from that midpoint (measured up to 3.3e-4 at |dv| in [4, 8)).
+# 5e-4 in fp16, 8x that in bf16 (3 fewer mantissa bits).
+GRAD_ENVELOPE = {torch.float16: F16_MAX, torch.bfloat16: 8 * F16_MAX}
+GRAD_MARGIN = {torch.float16: 5e-4, torch.bfloat16: 8 * 5e-4}
 
 
 def max_err(got, want) -> float:
@@ -55,6 +60,26 @@ def check_max(label: str, got, want, bound: float) -> float:
     print(f"{label}: max abs err {err:.3e} (bound {bound:.0e})", flush=True)
     assert err <= bound, f"{label}: max abs error {err:.3e} exceeds {bound:.0e}"
     return err
+
+
+def check_grads_pinned(tag: str, got, want, emulated, dtype, exact_m=None) -> list[tuple[float, float, float]]:
+    """16-bit gradients (dq, dk, dv) against the float32 reference `want`, bounded by
+    max(envelope, E + margin) with E the error of `emulated` (the reference's backward algorithm
+    with its rounding points on the same inputs, oracle.reference.rounded_backward with the
+    forward's O and M) against the same `want`. Prints the kernel's error, E, the bound, the
+    kernel's distance to the emulation and, when given, the error of `exact_m` (the same algorithm
+    from the exact log-sum-exp and the exactly rounded O: the reference's whole pipeline); returns
+    (err, E, bound) per gradient."""
+    out = []
+    for i, (name, g, w, e) in enumerate(zip(("dq", "dk", "dv"), got, want, emulated)):
+        err, emu = max_err(g, w), max_err(e, w)
+        bound = max(GRAD_ENVELOPE[dtype], emu + GRAD_MARGIN[dtype])
+        extra = f", reference pipeline (exact M) {max_err(exact_m[i], w):.3e}" if exact_m is not None else ""
+        print(f"{tag} {name}: max abs err {err:.3e}, reference algorithm {emu:.3e}, bound {bound:.3e}, "
+              f"kernel vs reference algorithm {max_err(g, e):.3e}{extra}", flush=True)
+        assert err <= bound, f"{tag} {name}: max abs error {err:.3e} exceeds {bound:.3e} (reference algorithm {emu:.3e})"
+        out.append((err, emu, bound))
+    return out
 
 
 def emulated_backward(q, k, v, o, m, do, causal, scale):

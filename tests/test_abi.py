@@ -97,6 +97,27 @@ def test_bwd_rejects_bad_config_for_both_tables():
     assert rc == 2 and "out of range" in _lib.last_error()
 
 
+@pytest.mark.parametrize("bad,msg", [
+    (dict(dk=24), "dk must be 16-byte aligned"),
+    (dict(dv=None), "dv is a null pointer"),
+    (dict(o=40), "o must be 16-byte aligned"),
+    (dict(m=None), "m and delta must not be null"),
+    (dict(delta=None), "m and delta must not be null"),
+    (dict(cfg=999), "out of range"),
+])
+def test_bwd_checks_every_argument_before_any_device_work(bad, msg):
+    """tattn_bwd validates all of its arguments, dK/dV's included, before it enqueues anything:
+    here (no GPU) the first device call would fail with a device error, so an argument error
+    that names dk, dv or o shows that no kernel (the dQ that runs first) was reached."""
+    lib = _lib.load()
+    st = (ctypes.c_int64 * 4)(1024, 64, 64, 1)
+    a = dict(q=16, k=16, v=16, o=16, do=16, dq=16, dk=16, dv=16, m=16, delta=16, cfg=-1)
+    a.update(bad)
+    rc = lib.tattn_bwd(a["q"], a["k"], a["v"], a["o"], a["do"], a["dq"], a["dk"], a["dv"], a["m"], a["delta"], st,
+                       1, 8, 512, 64, _lib.F16, 1, 0.125, a["cfg"], None)
+    assert rc in (1, 2) and msg in _lib.last_error()
+
+
 def test_bwd_noalloc_rejects_problems_past_its_workspace_before_launch():
     lib = _lib.load()
     st = (ctypes.c_int64 * 4)(1 << 20, 1 << 16, 64, 1)

@@ -66,14 +66,27 @@ def test_config_resolution():
     assert _resolve(_lib.K_FWD, 64, torch.float16, {"id": 2}, False, 128) == 2
     first = _lib.config_desc(_lib.K_FWD, 64, _lib.F16, 0)
     sel = {"BLOCK_M": first["block_m"], "BLOCK_N": first["block_n"], "waves": first["waves"]}
-    assert _resolve(_lib.K_FWD, 64, torch.float16, sel, False, 128) == 0
     with pytest.raises(ValueError, match="matches 0"):
         _resolve(_lib.K_FWD, 64, torch.float16, {"BLOCK_M": 7}, False, 128)
-    # A persistent entry shares its tiles with a pipelined one listed before it: "kind" picks it.
+    # A persistent entry shares its tiles with a pipelined one: "kind" chooses between them.
+    assert _resolve(_lib.K_FWD, 64, torch.float16, dict(sel, kind=first["kind"]), False, 128) == 0
     twin = dict(sel, kind=2)
     pid = _resolve(_lib.K_FWD, 64, torch.float16, twin, False, 128)
     desc = _lib.config_desc(_lib.K_FWD, 64, _lib.F16, pid)
     assert pid > 0 and desc["kind"] == 2 and desc["block_m"] == first["block_m"] and desc["ring"] in (4, 8)
+
+
+def test_ambiguous_config_dict_is_refused_and_kind_resolves_it():
+    """At head dim 64 the forward's 4 waves x 2 tiles exist as a pipelined entry (0) and as two
+    persistent ones (4: ring 8, 7: ring 4). Without "kind" the dict is refused, naming the
+    entries; with it, the lowest matching id of that kind is taken; "ring" narrows further."""
+    with pytest.raises(ValueError, match=r"entries \[0, 4, 7\] of kinds \[1, 2\]"):
+        _resolve(_lib.K_FWD, 64, torch.float16, {"waves": 4, "tiles": 2}, False, 4096)
+    assert _resolve(_lib.K_FWD, 64, torch.float16, {"waves": 4, "tiles": 2, "kind": 1}, False, 4096) == 0
+    assert _resolve(_lib.K_FWD, 64, torch.float16, {"waves": 4, "tiles": 2, "kind": 2}, False, 4096) == 4
+    assert _resolve(_lib.K_FWD, 64, torch.float16, {"waves": 4, "tiles": 2, "kind": 2, "ring": 4}, False, 4096) == 7
+    # One kind only: no ambiguity (the dK/dV table's 256-key entries 1 and 3 are both pipelined).
+    assert _resolve(_lib.K_BWD_DKDV, 64, torch.float16, {"BLOCK_N": 256}, False, 4096) == 1
 
 
 def test_autotune_off_by_default_and_cache_format(monkeypatch):

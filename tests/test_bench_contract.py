@@ -68,3 +68,26 @@ def test_default_contract_on_one_gpu():
     assert cpu["kind"] == "port" and cpu["cores"] >= 1 and cpu["value"] > 0 and cpu["sample"]
     assert cpu["threads"] == cpu["cores"] <= cpu["affinity_cores"] and cpu["thread_choice"]
     assert 0 < out["value"] < 2516.6
+
+
+@pytest.mark.gpu
+def test_backward_roofline_and_copy_yardstick():
+    """bench.py's backward-kernel roofline (dK/dV and dQ timed alone, tattn_bwd whole) and its
+    HBM copy yardstick: every length present, fractions of peak in (0, 1), the whole backward no
+    faster than its dK/dV alone, and a copy rate below the 8 TB/s HBM peak."""
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    data = {n: bench._inputs(n, torch.device("cuda:0")) for n in bench.SEQS}
+    roof = bench.backward_roofline(data, causal_modes=(False,))
+    assert [r["seq"] for r in roof["per_n"]] == list(bench.SEQS)
+    for r in roof["per_n"]:
+        print(r, flush=True)
+        for name in ("dkdv", "dq"):
+            assert 0 < r[name]["frac"] < 1 and r[name]["us"] > 0
+        assert 0 < r["tattn_bwd"]["frac"] < 1 and r["tattn_bwd"]["us"] >= 0.9 * r["dkdv"]["us"]
+    copy = bench.hbm_copy_tbps(64)
+    print(copy, flush=True)
+    assert 0.5 < copy["tbps"] < 8.0

@@ -360,28 +360,66 @@ def test_run_to_run_bitwise_identical(causal, dtype):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("shape", [(2, 3, 333, 64), (2, 4, 512, 64), (1, 8, 1024, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("causal", [False, True])
-def test_whole_backward_entry_point_matches_three_launches(dtype, causal):
-    """`tattn_bwd` (preprocess, dK/dV and dQ in one call) gives the bits of the three separate
-    entry points, and delta is the preprocess's rowsum(dO * O)."""
+def test_whole_backward_entry_point_matches_three_launches(dtype, causal, shape):
+    """`tattn_bwd` (in 16 bits: dQ computing delta itself, then dK/dV; two launches) gives the
+    bits of the reference's three launches in stream order (api.py:122-145): tattn_bwd_preprocess,
+    then tattn_bwd_dkdv and tattn_bwd_dq with the library's picks, and its delta is the
+    preprocess's, bit for bit. Shapes: a ragged length (pipelined dQ), 2 x 4 heads of 512 (Z*H a
+    multiple of 8: the persistent dQ) and head dim 128 (the paired-wave dQ)."""
     from tattn import _lib
-    from tattn.api import _DTYPES, _backward, _forward
+    from tattn.api import _DTYPES, _forward
 
-    q, k, v, do = (r((2, 3, 333, 64), dtype, 600 + s) for s in range(4))
+    z, h, n, d = shape
+    print(f"three launches: {shape} {dtype} causal={causal}", flush=True)
+    lib = _lib.load()
+    q, k, v, do = (r(shape, dtype, 600 + s) for s in range(4))
     o, m = _forward(q, k, v, causal, 0.125)
-    want = _backward(q, k, v, o, m, do, causal, 0.125)
-    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
-    delta = torch.empty((2, 3, 333), device=DEV, dtype=torch.float32)
-    rc = _lib.load().tattn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
-                               dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), m.data_ptr(), delta.data_ptr(),
-                               _lib.strides4(q), 2, 3, 333, 64, _DTYPES[dtype], int(causal), 0.125, -1,
-                               torch.cuda.current_stream().cuda_stream)
+    st, code, stream = _lib.strides4(q), _DTYPES[dtype], torch.cuda.current_stream().cuda_stream
+    delta3 = torch.full((z, h, n), float("nan"), device=DEV, dtype=torch.float32)
+    want = [torch.full_like(q, float("nan")) for _ in range(3)]
+    _lib.check(lib.tattn_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta3.data_ptr(), st, z, h, n, d, code, stream),
+               "tattn_bwd_preprocess")
+    _lib.check(lib.tattn_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), want[1].data_ptr(),
+                                  want[2].data_ptr(), m.data_ptr(), delta3.data_ptr(), st, z, h, n, d, code,
+                                  int(causal), 0.125, -1, stream), "tattn_bwd_dkdv")
+    _lib.check(lib.tattn_bwd_dq(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), want[0].data_ptr(),
+                                m.data_ptr(), delta3.data_ptr(), st, z, h, n, d, code, int(causal), 0.125, -1,
+                                stream), "tattn_bwd_dq")
+    dq, dk, dv = (torch.full_like(q, float("nan")) for _ in range(3))
+    delta = torch.full((z, h, n), float("nan"), device=DEV, dtype=torch.float32)
+    rc = lib.tattn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+                       dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), m.data_ptr(), delta.data_ptr(),
+                       st, z, h, n, d, code, int(causal), 0.125, -1, stream)
     _lib.check(rc, "tattn_bwd")
     torch.cuda.synchronize()
+    assert torch.equal(delta, delta3), "delta differs from the preprocess's"
     for name, got, ref in zip(("dq", "dk", "dv"), (dq, dk, dv), want):
         assert torch.equal(got, ref), name
     torch.testing.assert_close(delta, (do.float() * o.float()).sum(-1), atol=1e-5, rtol=1e-5)
+
+
+def test_whole_backward_rejects_bad_dk_before_writing_anything():
+    """A misaligned dk is refused before any launch: the dq, dv and delta buffers are untouched."""
+    from tattn import _lib
+
+    lib = _lib.load()
+    q, k, v, do = (r((2, 4, 512, 64), torch.float16, 610 + s) for s in range(4))
+    from tattn.api import _forward
+
+    o, m = _forward(q, k, v, True, 0.125)
+    dq, dv = torch.full_like(q, float("nan")), torch.full_like(q, float("nan"))
+    dk_buf = torch.full((q.numel() + 8,), float("nan"), device=DEV, dtype=torch.float16)
+    delta = torch.full((2, 4, 512), float("nan"), device=DEV, dtype=torch.float32)
+    rc = lib.tattn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), dq.data_ptr(),
+                       dk_buf.data_ptr() + 2, dv.data_ptr(), m.data_ptr(), delta.data_ptr(), _lib.strides4(q),
+                       2, 4, 512, 64, _lib.F16, 1, 0.125, -1, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 1 and "dk must be 16-byte aligned" in _lib.last_error()
+    assert dq.isnan().all() and dv.isnan().all() and delta.isnan().all() and dk_buf.isnan().all()
 
 
 @pytest.mark.parametrize("causal", [False, True])

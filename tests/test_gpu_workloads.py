@@ -21,9 +21,14 @@ materialised attention and its autograd on the same seeded inputs.
 
 Bounds: the envelope as flat maxima (max abs error <= 2e-3 in fp16 for outputs and gradients,
 <= 1e-5 in fp32; measured maxima are printed), plus the per-element envelope
-|err| <= 2e-3 + 2e-3 |ref| (fp32 1e-5 + 1e-5 |ref|). fp16 gradients of causal attention take the
-flat cap F16_CAUSAL_GRAD_MAX = 4e-3 instead (tests/helpers.py gives the mechanism and the measured
-error of the reference algorithm itself on these inputs).
+|err| <= 2e-3 + 2e-3 |ref| (fp32 1e-5 + 1e-5 |ref|). 16-bit causal gradients are held to
+max(2e-3, E + 5e-4) (bf16: 8x both), where E is the max abs error of the reference's own backward
+algorithm with its rounding points (oracle.reference.rounded_backward) on the same inputs (q, k,
+v, dO and the forward's O and M), against the same float32 reference: causal rows that see few
+keys reach |grad| of 4-8, where the 16-bit store alone costs up to half an ulp, and there no
+implementation with the reference's rounding points meets 2e-3. The margin is one last-place
+flip at the store (tests/helpers.py). Every such check prints the kernel's error beside E and
+beside the reference pipeline's error from the exact log-sum-exp.
 The float32 reference is computed a few heads at a time so its N x N matrices stay near 1 GiB."""
 
 import math
@@ -31,8 +36,8 @@ import math
 import pytest
 import torch
 
-from helpers import F16_CAUSAL_GRAD_MAX, F16_MAX, F32_MAX, check_max, emulated_backward, flip_cap, rand
-from oracle.reference import naive_attention, tiled_backward, tiled_forward
+from helpers import F16_MAX, F32_MAX, check_grads_pinned, check_max, emulated_backward, flip_cap, rand
+from oracle.reference import naive_attention, rounded_backward, tiled_backward, tiled_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -67,16 +72,30 @@ def _reference(q, k, v, do, causal):
     return outs
 
 
-def _check_all(tag, got, want, dtype, causal):
-    """Flat maxima and the per-element envelope for o, dq, dk, dv."""
+def _check_all(tag, got, want, dtype, causal, inputs=None):
+    """Flat maxima and the per-element envelope for o, dq, dk, dv. 16-bit causal gradients: the
+    bound pinned to the reference backward algorithm's own error on `inputs` (q, k, v, dO) and the
+    forward's O and M."""
     tol = F16_TOL if dtype == torch.float16 else F32_TOL
+    pinned = dtype != torch.float32 and causal
+    if pinned:
+        _pinned_grads(tag, got[1:], want[1:], *inputs, causal)
     for name, g, w in zip(("o", "dq", "dk", "dv"), got, want):
-        if dtype == torch.float16:
-            bound = F16_CAUSAL_GRAD_MAX if (causal and name != "o") else F16_MAX
-        else:
-            bound = F32_MAX
-        check_max(f"{tag} {name}", g, w, bound)
+        if not (pinned and name != "o"):
+            check_max(f"{tag} {name}", g, w, F16_MAX if dtype == torch.float16 else F32_MAX)
         torch.testing.assert_close(g, w, **tol, msg=lambda m: f"{name} {tag}: {m}")
+
+
+def _pinned_grads(tag, got, want, q, k, v, do, causal, scale=None):
+    """check_grads_pinned with the reference's backward algorithm run on the forward's saved O and
+    M (the inputs the kernels' backward gets), and the reference pipeline from the exact M beside."""
+    from tattn.api import _forward
+
+    scale = scale if scale is not None else q.shape[-1] ** -0.5
+    o, m = _forward(q, k, v, causal, scale)
+    emulated = rounded_backward(q, k, v, do, causal=causal, sm_scale=scale, o=o, lse=m)
+    exact_m = rounded_backward(q, k, v, do, causal=causal, sm_scale=scale)
+    check_grads_pinned(tag, got, want, emulated, q.dtype, exact_m)
 
 
 def _run(q, k, v, do, causal):
@@ -98,7 +117,7 @@ def test_edge_shapes_noncontiguous(d, n, causal, dtype):
     assert not q.is_contiguous() or n == 1
     got = _run(q, k, v, do, causal)
     want = _reference(q, k, v, do, causal)
-    _check_all(f"edge {dtype} d={d} n={n} causal={causal}", got, want, dtype, causal)
+    _check_all(f"edge {dtype} d={d} n={n} causal={causal}", got, want, dtype, causal, (q, k, v, do))
 
 
 @pytest.mark.parametrize("n", [512, 1024, 2048, 4096, 8192, 16384])
@@ -109,19 +128,24 @@ def test_full_size_fp16(n, causal):
     q, k, v, do = (torch.randn(b, 16, n, 64, device=DEV, dtype=torch.float16, generator=g) for _ in range(4))
     got = _run(q, k, v, do, causal)
     want = _reference(q, k, v, do, causal)
-    _check_all(f"full n={n} causal={causal}", got, want, torch.float16, causal)
+    _check_all(f"full n={n} causal={causal}", got, want, torch.float16, causal, (q, k, v, do))
 
 
 @pytest.mark.parametrize("d,dtype", [(128, torch.float16), (64, torch.bfloat16), (128, torch.bfloat16)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_other_head_dims_and_bf16_at_16k_tokens(d, dtype, causal):
     """The benchmark's token count at N=4096 (B=4, H=16) for head dim 128 and for bfloat16:
-    output and gradients against float32 autograd. bf16 tolerance: the fp16 bound x 8 (bf16
-    carries 3 fewer mantissa bits)."""
+    output and gradients against float32 autograd. Flat maxima: 2e-3 in fp16, 1.6e-2 in bf16 (the
+    fp16 bound x 8: bf16 carries 3 fewer mantissa bits); gradients pinned to the reference
+    algorithm's own error on the same inputs (check_grads_pinned), both masks. The per-element
+    envelope is checked beside them."""
     g = torch.Generator(device=DEV).manual_seed(4096 + d + int(causal))
     q, k, v, do = (torch.randn(4, 16, 4096, d, device=DEV, dtype=dtype, generator=g) for _ in range(4))
     got = _run(q, k, v, do, causal)
     want = _reference(q, k, v, do, causal)
+    tag = f"16k tokens d={d} {dtype} causal={causal}"
+    check_max(f"{tag} o", got[0], want[0], F16_MAX if dtype == torch.float16 else 8 * F16_MAX)
+    _pinned_grads(tag, got[1:], want[1:], q, k, v, do, causal)
     tol = F16_TOL if dtype == torch.float16 else {"atol": 1.6e-2, "rtol": 1.6e-2}
     for name, gt, w in zip(("o", "dq", "dk", "dv"), got, want):
         torch.testing.assert_close(gt, w, **tol, msg=lambda m: f"{name} d={d} {dtype} causal={causal}: {m}")
@@ -160,10 +184,11 @@ def test_long_context_scaled_inputs_and_memory(causal):
 def test_many_heads_short_rows(causal):
     """65,536 (batch, head) pairs of 24 tokens each (B=1024, H=64, D=16): the largest head count
     here. Output against float32 attention (flat 2e-3). Gradients against float32 autograd under
-    the flat causal cap (measured 3.7e-3 causal, 2.3e-3 not; the reference's rounding points
-    computed exactly give 3.5e-3 and 3.4e-3 on the same inputs: rows of one or two keys make
-    dP - delta cancel, so the rounding of the stored O and of dS dominates), and against the
-    backward with those rounding points within the envelope plus the capped flip allowance."""
+    the bound pinned to the reference algorithm's own error on the same inputs (rows of one or two
+    keys make dP - delta cancel, so the rounding of the stored O and of dS dominates: the
+    reference's rounding points computed exactly exceed 2e-3 here), and against the backward with
+    those rounding points from the kernel's O and M within the envelope plus the capped flip
+    allowance."""
     from tattn.api import _backward, _forward
 
     g = torch.Generator(device=DEV).manual_seed(24 + int(causal))
@@ -176,8 +201,8 @@ def test_many_heads_short_rows(causal):
     check_max(f"many heads causal={causal} o", o, ref.detach(), F16_MAX)
     torch.testing.assert_close(o.float(), ref.detach(), **F16_TOL)
     got = _backward(q, k, v, o, m, do, causal, scale)
-    for name, g_, w in zip(("dq", "dk", "dv"), got, (qr.grad, kr.grad, vr.grad)):
-        check_max(f"many heads causal={causal} {name} vs float32 autograd", g_, w, F16_CAUSAL_GRAD_MAX)
+    _pinned_grads(f"many heads causal={causal} vs float32 autograd", got, (qr.grad, kr.grad, vr.grad),
+                  q, k, v, do, causal, scale)
     want, flips = emulated_backward(q, k, v, o, m, do, causal, scale)
     cap = flip_cap(q.dtype, scale)
     for name, g_, w, bnd in zip(("dq", "dk", "dv"), got, want, flips):

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import exact
-from oracle.reference import LOG2E, flops, naive_attention, tiled_backward, tiled_forward
+from oracle.reference import LOG2E, flops, naive_attention, rounded_backward, tiled_backward, tiled_forward
 
 SHAPES = [(1, 1, 1, 16), (1, 2, 17, 16), (2, 1, 33, 32), (1, 1, 64, 64), (1, 2, 70, 16)]
 
@@ -109,6 +109,64 @@ def test_exact_lse_is_base2_logsumexp():
     s = (q @ k.transpose(-1, -2)) / 4.0
     want = torch.logsumexp(s, -1) / math.log(2.0)
     np.testing.assert_allclose(m, want.numpy(), atol=1e-12)
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("causal", [False, True])
+def test_rounded_backward_in_float32_is_the_exact_gradient(shape, causal):
+    """In float32 every rounding point of rounded_backward is the identity: it must give the
+    closed-form float64 gradients (a dropped term, a wrong sign, a transposed operand or mask
+    fails here). Small chunks exercise the chunking over leading dimensions."""
+    q, k, v, do = (rand(shape, s) for s in (110, 111, 112, 113))
+    got = rounded_backward(q, k, v, do, causal, max_scores=shape[-2] ** 2)
+    want = exact.attention_bwd(np64(q), np64(k), np64(v), np64(do), causal)
+    for g, w in zip(got, want):
+        assert g.dtype == torch.float32
+        np.testing.assert_allclose(g.numpy(), w, atol=2e-5, rtol=2e-5)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_rounded_backward_in_float16_rounds_and_stays_close(causal):
+    """In float16 the result is in float16, differs from the exact gradient (the roundings are
+    applied) by no more than the rounding of P, dS and the store can cause, and a different
+    non-default scale is honoured (against float64 at that scale)."""
+    q, k, v, do = (rand((2, 3, 40, 32), s, torch.float16) for s in (120, 121, 122, 123))
+    for scale in (None, 0.3):
+        got = rounded_backward(q, k, v, do, causal, sm_scale=scale)
+        want = exact.attention_bwd(np64(q), np64(k), np64(v), np64(do), causal, scale)
+        errs = []
+        for g, w in zip(got, want):
+            assert g.dtype == torch.float16
+            errs.append(np.abs(g.double().numpy() - w).max())
+        assert max(errs) < 6e-3, errs  # a few fp16 ulps at |grad| ~ 1-4
+        assert min(errs) > 1e-5, errs  # the roundings are really applied
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_rounded_backward_takes_a_stored_output_and_lse(causal):
+    """Given O and M (here from the tiled forward in float32, which match float64 at 1e-5), the
+    float32 result is still the exact gradient; given a wrong M (one row shifted by 1 in log2
+    units, i.e. that row's P doubled), that row's contributions change, so M is really used."""
+    q, k, v, do = (rand((1, 2, 37, 16), s) for s in (140, 141, 142, 143))
+    o, m = tiled_forward(q, k, v, causal)
+    got = rounded_backward(q, k, v, do, causal, o=o, lse=m)
+    want = exact.attention_bwd(np64(q), np64(k), np64(v), np64(do), causal)
+    for g, w in zip(got, want):
+        np.testing.assert_allclose(g.numpy(), w, atol=2e-5, rtol=2e-5)
+    m_bad = m.clone()
+    m_bad[0, 0, 20] -= 1.0
+    bad = rounded_backward(q, k, v, do, causal, o=o, lse=m_bad)
+    assert (bad[0][0, 0, 20] - got[0][0, 0, 20]).abs().max() > 1e-3  # dq of that row
+    assert torch.equal(bad[0][0, 1], got[0][0, 1])  # the other head is untouched
+
+
+def test_rounded_backward_single_key():
+    """One key: P = 1 exactly, so dV = dO exactly in float16 and dS = dP - delta = 0 up to the
+    float32 summation order of the two dot products."""
+    q, k, v, do = (rand((2, 3, 1, 64), s, torch.float16) for s in (130, 131, 132, 133))
+    dq, dk, dv = rounded_backward(q, k, v, do, True)
+    assert torch.equal(dv, do)
+    assert dq.abs().max().item() < 1e-4 and dk.abs().max().item() < 1e-4
 
 
 # ---- closed-form special cases (independent of any implementation's formula) --------------

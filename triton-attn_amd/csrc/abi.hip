@@ -344,41 +344,58 @@ int tattn_bwd_dq(const void* q, const void* k, const void* v, const void* dout, 
                      nullptr);
 }
 
-int tattn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, void* dq, void* dk,
-              void* dv, const float* m, float* delta, const int64_t strides[4], int64_t Z, int64_t H, int64_t N,
-              int64_t D, int dtype, int causal, float sm_scale, int config_id, void* stream) {
+// Checks every argument of the whole backward and resolves both kernels' table entries before
+// anything is enqueued, so a nonzero return from tattn_bwd means no work was launched.
+static int bwd_prepare(BwdParams& p, int* dk_id, int* dq_id, bool* fuse, const void* q, const void* k,
+                       const void* v, const void* o, const void* dout, void* dq, void* dk, void* dv, const float* m,
+                       float* delta, const int64_t strides[4], int64_t Z, int64_t H, int64_t N, int64_t D,
+                       int dtype, int causal, float sm_scale, int config_id) {
   int rc;
-  int dk_id = config_id, dq_id = config_id;
+  if ((rc = bwd_common(p, strides, Z, H, N, D, dtype, sm_scale))) return rc;
+  const int sz = dtype == TATTN_F32 ? 4 : 2;
+  if ((rc = check_tensor("q", q, strides, sz)) || (rc = check_tensor("k", k, strides, sz)) ||
+      (rc = check_tensor("v", v, strides, sz)) || (rc = check_tensor("o", o, strides, sz)) ||
+      (rc = check_tensor("do", dout, strides, sz)) || (rc = check_tensor("dq", dq, strides, sz)) ||
+      (rc = check_tensor("dk", dk, strides, sz)) || (rc = check_tensor("dv", dv, strides, sz)))
+    return rc;
+  if (!m || !delta) return set_error(TATTN_E_ARG, "m and delta must not be null");
   if (config_id >= 0) {
     // One id for both kernels, as the reference's `config=` (api.py:124-145): it must exist in both tables.
     if (config_id >= num_configs(TATTN_K_BWD_DKDV, D, dtype) || config_id >= num_configs(TATTN_K_BWD_DQ, D, dtype))
       return set_error(TATTN_E_CONFIG, "config id %d out of range for the backward tables", config_id);
   }
-  // When dQ runs a pipelined 16-bit kernel it computes delta itself (same bits as the preprocess)
-  // and stores it: dQ, then dK/dV, two launches and no separate pass over dO. Otherwise
-  // preprocess, dK/dV, dQ.
-  bool fuse = false;
-  {
-    BwdParams p{};
-    int qid;
-    if ((rc = bwd_common(p, strides, Z, H, N, D, dtype, sm_scale))) return rc;
-    if ((rc = resolve(TATTN_K_BWD_DQ, D, dtype, causal, N, Z * H, dq_id, &qid))) return rc;
-    const TileEntry* e = config_entry(TATTN_K_BWD_DQ, D, dtype, qid);
-    fuse = dtype != TATTN_F32 && e && e->pipe >= 1 && bwd_fits32(p, (int)D);
-  }
-  if (fuse) {
-    const int sz = dtype == TATTN_F32 ? 4 : 2;
-    if ((rc = check_tensor("o", o, strides, sz))) return rc;
-    if (!delta) return set_error(TATTN_E_ARG, "delta is a null pointer");
-    if ((rc = bwd_dq_call(q, k, v, dout, dq, m, delta, strides, Z, H, N, D, dtype, causal, sm_scale, dq_id, stream, o)))
-      return rc;
-    return tattn_bwd_dkdv(q, k, v, dout, dk, dv, m, delta, strides, Z, H, N, D, dtype, causal, sm_scale, dk_id, stream);
-  }
-  if ((rc = tattn_bwd_preprocess(o, dout, delta, strides, Z, H, N, D, dtype, stream))) return rc;
-  if ((rc = tattn_bwd_dkdv(q, k, v, dout, dk, dv, m, delta, strides, Z, H, N, D, dtype, causal, sm_scale, dk_id,
-                           stream)))
+  if ((rc = resolve(TATTN_K_BWD_DKDV, D, dtype, causal, N, Z * H, config_id, dk_id)) ||
+      (rc = resolve(TATTN_K_BWD_DQ, D, dtype, causal, N, Z * H, config_id, dq_id)))
     return rc;
-  return tattn_bwd_dq(q, k, v, dout, dq, m, delta, strides, Z, H, N, D, dtype, causal, sm_scale, dq_id, stream);
+  if ((rc = device_check())) return rc;
+  // When dQ runs a pipelined, persistent or paired-wave 16-bit kernel it computes delta itself
+  // (same bits as the preprocess) and stores it: dQ, then dK/dV, two launches and no separate
+  // pass over dO. Otherwise preprocess, dK/dV, dQ.
+  const TileEntry* e = config_entry(TATTN_K_BWD_DQ, D, dtype, *dq_id);
+  *fuse = dtype != TATTN_F32 && e && e->pipe >= 1 && bwd_fits32(p, (int)D);
+  p.q = q; p.k = k; p.v = v; p.o = o; p.dout = dout; p.dq = dq; p.dk = dk; p.dv = dv; p.m = m; p.delta = delta;
+  return TATTN_OK;
+}
+
+int tattn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, void* dq, void* dk,
+              void* dv, const float* m, float* delta, const int64_t strides[4], int64_t Z, int64_t H, int64_t N,
+              int64_t D, int dtype, int causal, float sm_scale, int config_id, void* stream) {
+  BwdParams p{};
+  int rc, dk_id = -1, dq_id = -1;
+  bool fuse = false;
+  if ((rc = bwd_prepare(p, &dk_id, &dq_id, &fuse, q, k, v, o, dout, dq, dk, dv, m, delta, strides, Z, H, N, D,
+                        dtype, causal, sm_scale, config_id)))
+    return rc;
+  const hipStream_t st = (hipStream_t)stream;
+  if (fuse) {
+    BwdParams pq = p;
+    pq.fuse_delta = 1;
+    if ((rc = launch_bwd_dq(pq, (int)D, dtype, causal != 0, dq_id, st))) return rc;
+    return launch_bwd_dkdv(p, (int)D, dtype, causal != 0, dk_id, st);
+  }
+  if ((rc = launch_bwd_preprocess(p, (int)D, dtype, st))) return rc;
+  if ((rc = launch_bwd_dkdv(p, (int)D, dtype, causal != 0, dk_id, st))) return rc;
+  return launch_bwd_dq(p, (int)D, dtype, causal != 0, dq_id, st);
 }
 
 int tattn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o, const void* dout, void* dq,

@@ -74,8 +74,9 @@ inline bool bwd_persist_fits(const TileEntry& e, int64_t ZH, int64_t N, bool cau
 // the pipelined kernel of the same tiles. Z*H a multiple of 8 (whole slices per XCD), N a
 // multiple of the block and of the ring period (whole unrolled groups), causal: an even number
 // of blocks per slice (pairs), a diagonal region of one or two ring periods, and one 32-row tile
-// per wave (the causal kernel with two tiles per wave needs more than the 256 registers a wave
-// has at two waves per SIMD; those entries run their pipelined twin for causal problems).
+// per wave or a ring of 4 (the causal kernel with two tiles per wave and a ring of 8 does not fit
+// the 256 registers a wave has at two waves per SIMD; those entries run their pipelined twin for
+// causal problems).
 constexpr bool fwd_persist_causal_ok(const TileEntry& e) {
   return (e.tiles == 1 || e.ring == 4) && (e.nw * e.tiles) % e.ring == 0 && e.nw * e.tiles / e.ring <= 2;
 }

@@ -105,8 +105,9 @@ def _resolve(kernel: int, d: int, dtype: torch.dtype, config: Config, causal: bo
     """Maps the reference-style `config=` to a table index: None -> the library's pick; an int is
     the index; a dict may give "id" or any of block_m / block_n / waves / tiles / kind / ring
     (upper-case BLOCK_M / BLOCK_N as in the reference are accepted) and must match at least one
-    entry; of several, the lowest index (a persistent entry, kind 2, shares its tiles with the
-    pipelined entry listed before it: give "kind": 2 to select it)."""
+    entry. Of several matches of one kind, the lowest index is taken; matches
+    of different kinds (a persistent entry shares its tiles with a pipelined one) are ambiguous
+    unless the dict gives "kind", and raise ValueError."""
     if config is None:
         return -1
     if isinstance(config, int):
@@ -116,10 +117,16 @@ def _resolve(kernel: int, d: int, dtype: torch.dtype, config: Config, causal: bo
     want = {k.lower(): int(v) for k, v in config.items()
             if k.lower() in ("block_m", "block_n", "waves", "tiles", "kind", "ring")}
     code = _DTYPES[dtype]
-    hits = [c for c in range(_lib.num_configs(kernel, d, code))
-            if all(_lib.config_desc(kernel, d, code, c)[key] == val for key, val in want.items())]
+    descs = [_lib.config_desc(kernel, d, code, c) for c in range(_lib.num_configs(kernel, d, code))]
+    hits = [c for c, desc in enumerate(descs) if all(desc[key] == val for key, val in want.items())]
     if not hits:
         raise ValueError(f"config {config} matches 0 {_lib.KERNEL_NAMES[kernel]} table entries")
+    kinds = sorted({descs[c]["kind"] for c in hits})
+    if len(kinds) > 1:
+        raise ValueError(
+            f"config {config} matches {_lib.KERNEL_NAMES[kernel]} table entries {hits} of kinds {kinds} "
+            f"(0 generic, 1 pipelined, 2 persistent, 3 paired-wave): give \"kind\" or \"id\""
+        )
     return hits[0]
 
 

@@ -130,8 +130,9 @@ def test_bwd_noalloc_rejects_problems_past_its_workspace_before_launch():
 @pytest.mark.parametrize("dtype", [_lib.F16, _lib.BF16])
 def test_picks_at_the_benchmark_lengths(n, dtype):
     """The static picks (tattn_pick_config, batch x heads a multiple of 8) at the benchmark
-    lengths, by kind: persistent forward and dQ wherever they fit, pipelined dK/dV at head dim
-    64, paired-wave backward at 128."""
+    lengths, by kind: persistent forward and dQ wherever they fit, the persistent 4-wave dK/dV at
+    head dim 64 for causal N < 4096 and the pipelined 8-wave one otherwise, paired-wave backward
+    at 128."""
     def kind(kernel, d, causal):
         return _lib.config_desc(kernel, d, dtype, _lib.pick_config(kernel, d, dtype, causal, n))
 
@@ -142,6 +143,9 @@ def test_picks_at_the_benchmark_lengths(n, dtype):
         assert f128["kind"] == 2 and f128["ring"] == 4
         assert (f128["waves"], f128["tiles"]) == ((8, 1) if n >= (4096 if causal else 2048) else (4, 1))
         dkdv64, dq64 = kind(_lib.K_BWD_DKDV, 64, causal), kind(_lib.K_BWD_DQ, 64, causal)
-        assert dkdv64["kind"] == 1 and dkdv64["waves"] == (4 if causal and n < 2048 else 8)
+        if causal and n < 4096:
+            assert dkdv64["kind"] == 2 and dkdv64["waves"] == 4
+        else:
+            assert dkdv64["kind"] == 1 and dkdv64["waves"] == 8
         assert dq64["kind"] == 2 and dq64["waves"] == 4
         assert kind(_lib.K_BWD_DKDV, 128, causal)["kind"] == 3 and kind(_lib.K_BWD_DQ, 128, causal)["kind"] == 3

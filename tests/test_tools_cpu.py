@@ -231,32 +231,42 @@ def own_scheduler_asm():
     return [diagnose.compile_asm(diagnose.CSRC / s) for s in ("fwd_persist_causal.hip", "bwd_dq_persist.hip", "bwd_split.hip")]
 
 
+@pytest.fixture(scope="module")
+def dkdv_persist_asm():
+    """The persistent dK/dV kernels' own translation unit (default scheduler)."""
+    return diagnose.compile_asm(diagnose.CSRC / "bwd_dkdv_persist.hip")
+
+
 @pytest.mark.skipif(not _have_hipcc(), reason="hipcc not installed")
-def test_no_kernel_spills_registers(fwd_asm, bwd_asm, own_scheduler_asm):
+def test_no_kernel_spills_registers(fwd_asm, bwd_asm, own_scheduler_asm, dkdv_persist_asm):
     """Every kernel instantiation the tile tables reach compiles without scratch (register
-    spills), except fp32 causal dK/dV at D=128 (a few bytes, not a performance path) and the
+    spills), except fp32 causal dK/dV at D=128 (a few bytes, not a performance path), the
     causal persistent forward with two tiles per wave (96 bytes under the iterative ILP
-    scheduler, which still runs it 3.5-4% faster than the default scheduler's 36-byte build)."""
+    scheduler, which still runs it 3.5-4% faster than the default scheduler's 36-byte build) and
+    the non-causal persistent dK/dV (at most 32 bytes: per-lane constants written once at the
+    start and reloaded once per key block, outside the step loop)."""
     allowed = {"dkdv_kernel<float, 128, 4, 1, 32, true, 1>",
                "fwd_persist_kernel<_Float16, 64, 4, 2, 2, true, 4>", "fwd_persist_kernel<__bf16, 64, 4, 2, 2, true, 4>"}
+    allowed_upto_32 = {f"dkdv_persist_kernel<{t}, 64, {nw}, 2, false>" for t in ("_Float16", "__bf16") for nw in (4, 8)}
     spills = []
-    for asm in (fwd_asm, bwd_asm, *own_scheduler_asm):
+    for asm in (fwd_asm, bwd_asm, *own_scheduler_asm, dkdv_persist_asm):
         for k in diagnose.isa_stats(asm, "_kernelI").values():
             name = k["name"].replace("tattn::", "").split("(")[0].removeprefix("void ")
-            if k.get("scratch_bytes_per_lane") and name not in allowed:
-                spills.append((name, k["scratch_bytes_per_lane"]))
+            sc = k.get("scratch_bytes_per_lane")
+            if sc and name not in allowed and not (name in allowed_upto_32 and sc <= 32):
+                spills.append((name, sc))
     assert not spills, spills
 
 
 @pytest.mark.skipif(not _have_hipcc(), reason="hipcc not installed")
-def test_each_kernel_lives_in_one_translation_unit(fwd_asm, bwd_asm, own_scheduler_asm):
+def test_each_kernel_lives_in_one_translation_unit(fwd_asm, bwd_asm, own_scheduler_asm, dkdv_persist_asm):
     """A kernel instantiated by two translation units would reach the library twice, built with
     different scheduler flags; the launchers keep each family in exactly one unit."""
     import collections
     import re
 
     seen = collections.Counter()
-    for asm in (fwd_asm, bwd_asm, *own_scheduler_asm):
+    for asm in (fwd_asm, bwd_asm, *own_scheduler_asm, dkdv_persist_asm):
         seen.update(set(re.findall(r"^\s*\.amdhsa_kernel (\S+)", asm, re.M)))
     dups = [k for k, n in seen.items() if n > 1]
     assert not dups, dups
@@ -264,3 +274,5 @@ def test_each_kernel_lives_in_one_translation_unit(fwd_asm, bwd_asm, own_schedul
     assert causal2 and all("fwd_persist_kernel" in k for k in causal2)
     assert dq_persist and all("dq_persist_kernel" in k for k in dq_persist)
     assert split and all("_split_kernel" in k for k in split)
+    dkdv_persist = set(re.findall(r"^\s*\.amdhsa_kernel (\S+)", dkdv_persist_asm, re.M))
+    assert dkdv_persist and all("dkdv_persist_kernel" in k for k in dkdv_persist)

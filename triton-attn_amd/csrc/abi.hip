@@ -124,9 +124,13 @@ int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N, int64_t
       if (causal) return N >= 4096 ? 0 : 1;
       if (D == 64) return N >= 4096 ? 3 : N >= 1024 ? 0 : 1;
       return D == 16 && N < 2048 ? 1 : 0;
-    case TATTN_K_BWD_DKDV:  // pipelined, 8 waves (256 keys); causal N < 2048: 4 waves (128 keys)
+    case TATTN_K_BWD_DKDV:  // causal N < 4096: persistent 4 waves where it fits; else pipelined, 8 waves
+                            // (256 keys), causal N < 2048: 4 waves (128 keys). Picked on the whole
+                            // forward + backward: there the persistent entries lose non-causal (the
+                            // dQ pass leaves this kernel's inputs in the caches).
       if (D == 128) return 2;  // paired waves: two per SIMD, where one wave per tile needs all 512 registers
       if (D != 64) return 0;
+      if (causal && N < 4096 && bwd_persist_fits(DkdvTable<_Float16, 64>::e[5], ZH, N, true)) return 5;
       if (!causal) return 1;
       return N >= 2048 ? 1 : 0;
     case TATTN_K_BWD_DQ:  // persistent 4 waves where it fits; else 4 waves (8 for non-causal 2048 <= N < 8192)

@@ -633,6 +633,11 @@ static int launch_dkdv_entry(const BwdParams& p0, bool causal, hipStream_t st) {
       dkdv_kernel<T, D, 4, 1, 32, false, D == 128 ? 1 : 2><<<g2, dim3(256), 0, st>>>(p);
   } else if constexpr (e.pipe >= 1) {
     static_assert(sizeof(T) == 2 && D <= 128 && (e.tiles == 1 || D <= 64) && e.other == 32, "pipelined dK/dV shape");
+    if constexpr (e.pipe == 2) {
+      static_assert(e.tiles == 1 && D <= 64, "persistent dK/dV shape");
+      if (slice_fits32(p, D) && bwd_persist_fits(e, (int64_t)p.Z * p.H, p.N, causal))  // own translation unit
+        return launch_dkdv_persist(p0, D, std::is_same_v<T, bf16> ? 2 : 0, I, causal, st);
+    }
     if (slice_fits32(p, D)) {
       if (causal)
         dkdv_pipe_kernel<T, D, e.nw, e.tiles, e.occ, true><<<grid, block, 0, st>>>(p);
@@ -753,6 +758,7 @@ int launch_bwd_dq(const BwdParams& p, int D, int dtype, bool causal, int id, hip
 int dkdv_lds_bytes(int D, int dtype, const TileEntry& e) {
   const int r = dtype != 1 ? (D < 32 ? 64 : 2 * D) : 4 * D + 16;
   if (e.pipe == 3) return 4 * (2 * 32 * r + 256) + 2 * 4 * 32 * 32 * 4;  // ring + P exchange buffers
+  if (e.pipe == 2) return 4 * (2 * 32 * r + 256) + e.nw * 2 * 32 * r;     // ring + K/V staging tiles
   if (e.pipe) return 4 * (2 * 32 * r + 256);
   return 2 * (2 * e.other * r + 2 * e.other * 4);
 }

@@ -38,6 +38,9 @@ int launch_fwd_persist_causal2(const FwdParams& p, int D, int dtype, int config_
 // Persistent dQ (bwd_dq_persist.hip): runs entry `config_id` of the dQ table; the caller has
 // checked bwd_persist_fits and bwd_fits32.
 int launch_dq_persist(const BwdParams& p, int D, int dtype, int config_id, bool causal, hipStream_t st);
+// Persistent dK/dV (bwd_dkdv_persist.hip): runs entry `config_id` of the dK/dV table; the caller
+// has checked bwd_persist_fits and bwd_fits32.
+int launch_dkdv_persist(const BwdParams& p, int D, int dtype, int config_id, bool causal, hipStream_t st);
 // Paired-wave backward (bwd_split.hip): dK/dV (dkdv = true) or dQ with 128 rows per workgroup,
 // p.n_blocks set by the caller; the caller has checked bwd_fits32.
 int launch_split(const BwdParams& p, int D, int dtype, bool dkdv, bool causal, hipStream_t st);

@@ -66,7 +66,8 @@ namespace tattn {
 template <typename T, int D> struct DkdvTable;
 TATTN_TABLE16(DkdvTable, 16, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {4, 2, 32, 2, 0})
 TATTN_TABLE16(DkdvTable, 32, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 64, 2, 0}, {4, 1, 32, 2, 0}, {4, 2, 32, 2, 0})
-TATTN_TABLE16(DkdvTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 32, 2, 0}, {4, 2, 32, 1, 1}, {8, 1, 32, 2, 3})
+TATTN_TABLE16(DkdvTable, 64, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {4, 1, 32, 2, 0}, {4, 2, 32, 1, 1}, {8, 1, 32, 2, 3},
+              {4, 1, 32, 2, 2}, {8, 1, 32, 2, 2})
 TATTN_TABLE16(DkdvTable, 128, {4, 1, 32, 1, 1}, {4, 1, 32, 1, 0}, {8, 1, 32, 2, 3})
 TATTN_TABLE(DkdvTable, float, 16, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})
 TATTN_TABLE(DkdvTable, float, 32, {4, 1, 32, 2, 0}, {4, 1, 64, 2, 0})

@@ -18,7 +18,8 @@ CSRC = PKG.parent / "csrc"
 REPO = PKG.parent.parent
 INCLUDE = REPO / "include"
 LIB = PKG / "libtattn_hip.so"
-SOURCES = ["abi.hip", "fwd.hip", "fwd_persist_causal.hip", "bwd.hip", "bwd_dq_persist.hip", "bwd_split.hip"]
+SOURCES = ["abi.hip", "fwd.hip", "fwd_persist_causal.hip", "bwd.hip", "bwd_dq_persist.hip", "bwd_dkdv_persist.hip",
+           "bwd_split.hip"]
 # Per-source flags. fwd.hip: keep each step's softmax work in the step that issues the
 # independent MFMAs it interleaves with (machine sinking would move it to its first use).
 # fwd_persist_causal.hip (persistent causal forward, two tiles per wave), bwd_dq_persist.hip

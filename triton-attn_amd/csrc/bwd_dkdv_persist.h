@@ -398,8 +398,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_persist_kernel(const BwdPar
     kw0 = kb * BNK + 32 * wu;
     cur = src_of(t + 1);
   }
-  // No LDS DMA may still be in flight when the workgroup's LDS is released.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  // No LDS DMA is in flight here: the last block starts none, and every earlier one was read out
+  // of its staging tile. The waves end without waiting for the dK / dV stores.
 }
 
 }  // namespace tattn

@@ -486,6 +486,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_persist_kernel(const FwdPara
     group(R * gi, std::true_type{}, CAUSAL ? SUB - R : -1);  // the block's last group
     // Drain: PV of the block's last step (V slot R - 1), then the block's O and M.
     if (!CAUSAL || wu * QT + QT - 1 >= SUB - 1) pv_mma(pa, R - 1);
+    // The workgroup's last block: its last DMAs (zero-byte descriptors past the end, they touch no
+    // memory) must land before the workgroup's LDS is released. Waiting here, before the O and M
+    // stores, lets the waves end without waiting for those stores.
+    if (t + 1 == nseg) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     {
       T* O = (T*)p.o + (int64_t)(zh / p.H) * p.so[0] + (int64_t)(zh % p.H) * p.so[1];
       float* M = p.m ? p.m + (int64_t)zh * N : nullptr;
@@ -522,8 +526,6 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_persist_kernel(const FwdPara
     vrs_n = slice_v(t + 2);
     begin_block();
   }
-  // No LDS DMA may still be in flight when the workgroup's LDS is released.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 }
 
 // Persistent forward: grid of one workgroup per resident slot (at most), the work split per XCD

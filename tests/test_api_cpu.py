@@ -85,8 +85,10 @@ def test_ambiguous_config_dict_is_refused_and_kind_resolves_it():
     assert _resolve(_lib.K_FWD, 64, torch.float16, {"waves": 4, "tiles": 2, "kind": 1}, False, 4096) == 0
     assert _resolve(_lib.K_FWD, 64, torch.float16, {"waves": 4, "tiles": 2, "kind": 2}, False, 4096) == 4
     assert _resolve(_lib.K_FWD, 64, torch.float16, {"waves": 4, "tiles": 2, "kind": 2, "ring": 4}, False, 4096) == 7
-    # One kind only: no ambiguity (the dK/dV table's 256-key entries 1 and 3 are both pipelined).
-    assert _resolve(_lib.K_BWD_DKDV, 64, torch.float16, {"BLOCK_N": 256}, False, 4096) == 1
+    # Several matches of one kind: the lowest id (the dQ table's generic 128-row entries 2 and 3).
+    assert _resolve(_lib.K_BWD_DQ, 64, torch.float16, {"BLOCK_M": 128, "kind": 0}, False, 4096) == 2
+    with pytest.raises(ValueError, match="give"):
+        _resolve(_lib.K_BWD_DKDV, 64, torch.float16, {"BLOCK_N": 256}, False, 4096)
 
 
 def test_autotune_off_by_default_and_cache_format(monkeypatch):

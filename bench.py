@@ -12,7 +12,7 @@ kernel (HIP events around every forward launch of the timed steps, on the launch
 per-N sweep (forward, causal and non-causal; fwd+bwd, causal and non-causal, with peak extra
 memory) timed like the reference's tables (tattn.timing.do_bench: cache flushed before each
 call, median over ~100 ms), the roofline of the two backward kernels per N and mask
-(`roofline.bwd`: dK/dV and dQ each timed alone through the C ABI, and tattn_bwd whole), a
+(`roofline.bwd`: HIP events around warm launches of tattn_bwd whole and of its dK/dV alone), a
 measured HBM yardstick (`roofline.hbm_copy_tbps`: a 256 MiB device copy, the memory analog of
 the reference's GEMM yardstick, bench/bench.py:173-175), the accuracy of each shape as the
 reference's benchmark measures it (bench/bench.py:128-171: forward max / mean abs error against
@@ -207,22 +207,33 @@ def full_tensor_causal_grads(data, n: int) -> list[dict]:
             for name, e, r, pp in zip(("dq", "dk", "dv"), err, emu, pipe)]
 
 
-def backward_roofline(data, causal_modes=(False, True)) -> dict:
-    """The two backward kernels of the default path, each timed on its own with the reference's
-    timer (tattn.timing.do_bench: HIP events on the launch stream, 256 MB cache flush before each
-    call, median) through the C ABI with the library's picks: dK/dV (tattn_bwd_dkdv) and dQ
-    (tattn_bwd_dq, reading the preprocess's delta), plus tattn_bwd as one call (dQ computing delta
-    itself, then dK/dV). Executed matrix-core work per launch: dK/dV 4 GEMMs per 32 x 32 block
-    (S, dP, dV, dK) = 2 x the forward's flops, dQ 3 (S, dP, dQ) = 1.5 x; the reference's
-    convention counts the backward as 2.5 x the forward (bench/bench.py:31-35)."""
+def backward_roofline(data, causal_modes=(False, True), reps: int = 10) -> dict:
+    """The two backward kernels of the default path, timed like the forward roofline: HIP events
+    around every launch on the launch stream, back to back with the inputs resident (3 untimed
+    launches first), average duration. Per N and mask: tattn_bwd as one call (dQ computing delta
+    itself, then dK/dV: the backward every fwd+bwd cell runs) and tattn_bwd_dkdv alone with the
+    same pick; the fused dQ is their difference. Executed matrix-core work per launch: dK/dV 4
+    GEMMs per 32 x 32 block (S, dP, dV, dK) = 2 x the forward's flops, dQ 3 (S, dP, dQ) = 1.5 x;
+    the reference's convention counts the backward as 2.5 x the forward (bench/bench.py:31-35)."""
     import torch
 
     from tattn import _lib
     from tattn.api import _forward
-    from tattn.timing import do_bench
 
     lib = _lib.load()
     scale = 1.0 / math.sqrt(DIM)
+
+    def avg_ms(fn) -> float:
+        for _ in range(3):
+            fn()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for e0, e1 in ev:
+            e0.record()
+            fn()
+            e1.record()
+        torch.cuda.synchronize()
+        return sum(e0.elapsed_time(e1) for e0, e1 in ev) / reps
+
     rows = []
     for causal in causal_modes:
         for n in SEQS:
@@ -233,30 +244,26 @@ def backward_roofline(data, causal_modes=(False, True)) -> dict:
             delta = torch.empty((b, HEADS, n), device=q.device, dtype=torch.float32)
             dq, dk, dv = (torch.empty_like(q) for _ in range(3))
             shape = (b, HEADS, n, DIM, _lib.F16, int(causal), scale, -1, stream)
-            _lib.check(lib.tattn_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta.data_ptr(), st, b, HEADS, n, DIM,
-                                                _lib.F16, stream), "tattn_bwd_preprocess")
-
-            def dkdv() -> None:
-                lib.tattn_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), dk.data_ptr(),
-                                   dv.data_ptr(), m.data_ptr(), delta.data_ptr(), st, *shape)
-
-            def dqk() -> None:
-                lib.tattn_bwd_dq(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), dq.data_ptr(),
-                                 m.data_ptr(), delta.data_ptr(), st, *shape)
 
             def whole() -> None:
-                lib.tattn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), dq.data_ptr(),
-                              dk.data_ptr(), dv.data_ptr(), m.data_ptr(), delta.data_ptr(), st, *shape)
+                _lib.check(lib.tattn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+                                         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), m.data_ptr(), delta.data_ptr(),
+                                         st, *shape), "tattn_bwd")
+
+            def dkdv() -> None:
+                _lib.check(lib.tattn_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), dk.data_ptr(),
+                                              dv.data_ptr(), m.data_ptr(), delta.data_ptr(), st, *shape),
+                           "tattn_bwd_dkdv")
 
             f = flops(b, HEADS, n, DIM, causal, "fwd")
-            t_kv, t_q, t_all = do_bench(dkdv), do_bench(dqk), do_bench(whole)
+            t_all = avg_ms(whole)  # also leaves delta computed for dkdv()
+            t_kv = avg_ms(dkdv)
+            t_q = max(t_all - t_kv, 1e-6)
             row = {"seq": n, "batch": b, "causal": causal}
-            for name, ms, work in (("dkdv", t_kv, 2.0 * f), ("dq", t_q, 1.5 * f)):
+            for name, ms, work, kern in (("dkdv", t_kv, 2.0 * f, _lib.K_BWD_DKDV), ("dq", t_q, 1.5 * f, _lib.K_BWD_DQ)):
                 tf = work / (ms * 1e-3) / 1e12
-                row[name] = {"entry": _lib.pick_config(_lib.K_BWD_DKDV if name == "dkdv" else _lib.K_BWD_DQ,
-                                                       DIM, _lib.F16, causal, n),
-                             "us": round(1e3 * ms, 2), "exec_tflops": round(tf, 1),
-                             "frac": round(tf / PEAK_F16_TFLOPS, 4)}
+                row[name] = {"entry": _lib.pick_config(kern, DIM, _lib.F16, causal, n), "us": round(1e3 * ms, 2),
+                             "exec_tflops": round(tf, 1), "frac": round(tf / PEAK_F16_TFLOPS, 4)}
             counted = 2.5 * f / (t_all * 1e-3) / 1e12
             row["tattn_bwd"] = {"us": round(1e3 * t_all, 2), "counted_tflops": round(counted, 1),
                                 "frac": round(counted / PEAK_F16_TFLOPS, 4)}
@@ -264,32 +271,32 @@ def backward_roofline(data, causal_modes=(False, True)) -> dict:
             print(json.dumps({"bwd_roofline": row}), file=sys.stderr, flush=True)
             del o, m, delta, dq, dk, dv
     return {"bound": "mfma", "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
-            "timer": "cold-cache median per call (tattn.timing.do_bench), HIP events on the launch stream",
+            "timer": f"HIP events around each launch on the launch stream, {reps} back-to-back launches after 3 untimed, "
+                     "inputs resident; dq = tattn_bwd - tattn_bwd_dkdv (dQ computes delta itself)",
             "work": "dkdv: 2x forward flops, dq: 1.5x (executed GEMMs); tattn_bwd: 2.5x (the reference's count)",
             "per_n": rows}
 
 
-def hbm_copy_tbps(mib: int = 256) -> dict:
-    """Measured HBM bandwidth yardstick: a device-to-device copy of `mib` MiB (torch's copy kernel),
-    HIP events, median of 20 after 3 warm-ups; bytes moved = read + write."""
+def hbm_copy_tbps(mib: int = 256, reps: int = 20) -> dict:
+    """Measured HBM bandwidth yardstick: device-to-device copies of `mib` MiB (torch's copy, the
+    runtime's copy kernel), HIP events around each of `reps` back-to-back copies after 3 untimed
+    ones, average; bytes moved = read + write."""
     import torch
 
     src = torch.empty(mib * 2**18, device="cuda", dtype=torch.float32)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
-    times = []
-    for _ in range(20):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in ev:
         e0.record()
         dst.copy_(src)
         e1.record()
-        e1.synchronize()
-        times.append(e0.elapsed_time(e1))
-    ms = statistics.median(times)
+    torch.cuda.synchronize()
+    ms = sum(e0.elapsed_time(e1) for e0, e1 in ev) / reps
     del src, dst
     return {"mib": mib, "us": round(1e3 * ms, 2), "tbps": round(2 * mib * 2**20 / (ms * 1e-3) / 1e12, 3),
-            "peak_tbps": 8.0}
+            "peak_tbps": 8.0, "timer": f"HIP events around each of {reps} back-to-back copies, average"}
 
 
 def main() -> int:

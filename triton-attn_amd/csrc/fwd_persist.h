@@ -154,17 +154,22 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_persist_kernel(const FwdPara
     piece(pp, p.sk[2], true, kgo[t]);
     piece(pp, p.sv[2], false, vgo[t]);
   }
+  // The tile's offset (wave-uniform) goes into the scalar offset of the load, so one lane offset
+  // serves every step: offsets per step position summed into VGPRs were held across the block
+  // loop and spilled in the causal two-tile kernel. Every tile read lies inside its slice (N is a
+  // multiple of the block and the ring period); past the last block the descriptor has zero bytes
+  // and each load reads zeros.
   auto dma_k = [&](__amdgpu_buffer_rsrc_t rs, int kt, int slot) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < CPK; ++t)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (TATTN_LDS void*)(kbuf(slot) + kpc[t]), 16,
-                                               (int)(kgo[t] + (uint32_t)kt * k_step), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (TATTN_LDS void*)(kbuf(slot) + kpc[t]), 16, (int)kgo[t],
+                                               (int)((uint32_t)kt * k_step), 0, 0);
   };
   auto dma_v = [&](__amdgpu_buffer_rsrc_t rs, int vt, int slot) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < CPV; ++t)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (TATTN_LDS void*)(vbuf(slot) + kpc[t]), 16,
-                                               (int)(vgo[t] + (uint32_t)vt * v_step), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (TATTN_LDS void*)(vbuf(slot) + kpc[t]), 16, (int)vgo[t],
+                                               (int)((uint32_t)vt * v_step), 0, 0);
   };
   // End of a step: the DMAs of the previous step have landed (OUTSTANDING = memory operations
   // issued after them), this wave's LDS reads are done, then the barrier.
@@ -232,10 +237,16 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_persist_kernel(const FwdPara
   };
 
   // Diagonal 32x32 tile (first key = first row): register r holds key offset kappa(r, h2) of row
-  // offset l32; keys past the row are hidden.
-  bool diag_hide[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) diag_hide[r] = CAUSAL && kappa(r, h2) > l32;
+  // offset l32; keys past the row are hidden: kappa(r, h2) > l32, i.e. l32 - 8 h2 below
+  // 16 (r / 8) + r % 8. One compare per use: sixteen lane masks computed once would be held
+  // across the block loop in 32 SGPRs (spilled to VGPR lanes, which pushed VGPRs to scratch).
+  // The empty asm keeps the compiler from hoisting the compares back out of the loop.
+  const int diag_x = l32 - 8 * h2;
+  auto diag_hide = [&](int r) __attribute__((always_inline)) {
+    int x = diag_x;
+    asm volatile("" : "+v"(x));
+    return CAUSAL && x < 16 * (r >> 3) + (r & 7);
+  };
   // Probabilities of one tile against the row max as it stands; hidden keys get probability 0
   // (after the exponential). Returns the lane's sum of the rounded probabilities.
   auto tile_probs = [&](const f32x16& st, V8* pt, float nm, auto diag_tag) __attribute__((always_inline)) {
@@ -249,8 +260,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_persist_kernel(const FwdPara
         float e0 = fast_exp2(__builtin_fmaf(st[8 * sg + i], c, nm));
         float e1 = fast_exp2(__builtin_fmaf(st[8 * sg + i + 1], c, nm));
         if constexpr (DIAG) {
-          e0 = diag_hide[8 * sg + i] ? 0.0f : e0;
-          e1 = diag_hide[8 * sg + i + 1] ? 0.0f : e1;
+          e0 = diag_hide(8 * sg + i) ? 0.0f : e0;
+          e1 = diag_hide(8 * sg + i + 1) ? 0.0f : e1;
         }
         const V2 pr = H::pack(e0, e1);
         acc_s = H::sum2(pr, acc_s);
@@ -266,7 +277,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_persist_kernel(const FwdPara
     constexpr bool DIAG = decltype(diag_tag)::value;
     float mx = -__builtin_inff();
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mx = (DIAG && diag_hide[r]) ? mx : __builtin_fmaxf(mx, st[r] * c);
+    for (int r = 0; r < 16; ++r) mx = (DIAG && diag_hide(r)) ? mx : __builtin_fmaxf(mx, st[r] * c);
     return max_halves(mx);
   };
   // Tile j of a step in the block's diagonal region: its place against the diagonal in 32-row

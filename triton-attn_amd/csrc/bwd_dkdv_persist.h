@@ -312,10 +312,6 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_persist_kernel(const BwdPar
     if (!CAUSAL || wu == 0) qk(sa, da, 0);
 
     // One unmasked step (local index i, i % 4 == IV). LASTG: the block's last group (its steps 2
-    // and 3 load the next block's stages 0 and 1; no S in step 3). Steps i < PIECES also start one
-    // piece each of the next block's K and V rows for this wave (the loads of the same step and
-    // of every later one are waited for in order, so the pieces land within the block).
-    // One unmasked step (local index i, i % 4 == IV). LASTG: the block's last group (its steps 2
     // and 3 load the next block's stages 0 and 1; no S in step 3). Steps i < PIECES also start
     // piece i of the next block's K and V rows for this wave, after the step's own loads (so the
     // step's wait leaves them in flight; later steps' waits, in issue order, see them land within

@@ -540,15 +540,18 @@ def test_one_hip_runtime_mapped():
     assert any("libtattn_hip.so" in line for line in maps)
 
 
+@pytest.mark.parametrize("shape", [(2, 3, 300, 64), (2, 4, 512, 64)])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_inference_path_matches_autograd_path(causal, dtype):
+def test_inference_path_matches_autograd_path(causal, dtype, shape):
     """Without grad, attention keeps no autograd state and stores no log-sum-exp (tattn_fwd with
-    m = NULL); its output is bitwise the autograd path's."""
+    m = NULL); its output is bitwise the autograd path's. The second shape runs the persistent
+    forward, whose inference launch (16-bit, non-causal) streams K/V with the non-temporal cache
+    policy: a cache hint only, so the output is the same bits."""
     from tattn import attention
     from tattn.api import _forward
 
-    q, k, v = (r((2, 3, 300, 64), dtype, s) for s in (100, 101, 102))
+    q, k, v = (r(shape, dtype, s) for s in (100, 101, 102))
     qg = q.clone().requires_grad_()
     o_grad = attention(qg, k, v, causal=causal)
     with torch.no_grad():

@@ -267,7 +267,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_persist_kernel(const BwdPar
       const int row = j / CPRO, cc = j % CPRO;
       if (row < 32) {
         const u32x4 v = *reinterpret_cast<const TATTN_LDS u32x4*>((const TATTN_LDS char*)wb + row * RB + 16 * cc);
-        st16(dst + (int64_t)(kw0 + row) * rs + 8 * cc, v);
+        st16_stream(dst + (int64_t)(kw0 + row) * rs + 8 * cc, v);
       }
     }
   };

@@ -361,7 +361,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void dkdv_pipe_kernel(const BwdParams
       const int key = key0 + row;
       if (row < 32 && key < N) {
         const u32x4 v = *reinterpret_cast<const TATTN_LDS u32x4*>((const TATTN_LDS char*)wb + row * RB + 16 * cc);
-        st16(dst + (int64_t)key * rs + 8 * cc, v);
+        st16_stream(dst + (int64_t)key * rs + 8 * cc, v);
       }
     }
   };

@@ -320,7 +320,7 @@ __global__ __launch_bounds__(512, 2) void dkdv_split_kernel(const BwdParams p) {
       const int key = kw0 + row;
       if (row < 32 && key < N) {
         const u32x4 v = *reinterpret_cast<const TATTN_LDS u32x4*>((const TATTN_LDS char*)wb + row * RB + 16 * cc);
-        st16(dst + (int64_t)key * rs + 8 * cc, v);
+        st16_stream(dst + (int64_t)key * rs + 8 * cc, v);
       }
     }
   }

@@ -159,6 +159,11 @@ __device__ __host__ __forceinline__ constexpr int kappa(int r, int h) {
 // 16-byte global load / store helpers (addresses are 16-byte aligned by construction).
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+// A 16-byte store with the non-temporal cache policy, for outputs written once as whole 128-byte
+// rows by the last kernel that touches them (dK, dV).
+__device__ __forceinline__ void st16_stream(void* p, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
 
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element (i % 4) of the
 // 8-byte rows addressed by lanes (i / 4) + 4t of its group, t = 0..3. Addressing lane s of a

@@ -766,6 +766,7 @@ int dkdv_lds_bytes(int D, int dtype, const TileEntry& e) {
 int dq_lds_bytes(int D, int dtype, const TileEntry& e) {
   const int r = dtype != 1 ? (D < 32 ? 64 : 2 * D) : 4 * D + 16;
   if (e.pipe == 3) return 4 * (2 * 32 * r) + 2 * 4 * 32 * 32 * 4;  // ring + P exchange buffers
+  if (e.pipe == 2) return 4 * (2 * 32 * r) + e.nw * 32 * r;  // ring + per-wave dQ rows
   if (e.pipe) return 4 * (2 * 32 * r);
   return 2 * (2 * e.other * r);
 }

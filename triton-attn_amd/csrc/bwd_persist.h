@@ -41,6 +41,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_persist_kernel(const BwdParam
   constexpr int SPI = CAUSAL ? 2 : 1;
   static_assert(NW % 4 == 0, "diagonal steps in whole groups of four");
   __shared__ __attribute__((aligned(16))) char smem[B::NST * STAGE];
+  // Per wave: its 32 dQ rows on their way out (whole-row stores, below).
+  __shared__ __attribute__((aligned(16))) char dqs[NW * 32 * B::RB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6, h2 = lane >> 5, l32 = lane & 31;
@@ -269,8 +271,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_persist_kernel(const BwdParam
     // Drain: dQ of the block's last step (stage 3; the last wave's diagonal), then the store.
     if (!CAUSAL || NW - 1 <= w) dq_mma(ea, 3);
     {
-      const int64_t hoff = (int64_t)(zh / p.H) * p.s[0] + (int64_t)(zh % p.H) * p.s[1];
-      T* row = (T*)p.dq + hoff + (int64_t)q * rs;
+      // dQ (scaled, rounded) through the wave's LDS rows, then stored as whole 128-byte rows with
+      // the non-temporal policy: nothing in the backward reads dQ. (Wave-local rows: no barrier.
+      // The row index is computed here, not held across the block loop.)
+      TATTN_LDS char* wt = (TATTN_LDS char*)dqs + w * 32 * B::RB;
+      int rl = l32;
+      asm volatile("" : "+v"(rl));
 #pragma unroll
       for (int u = 0; u < DT; ++u)
 #pragma unroll
@@ -280,9 +286,21 @@ __global__ __launch_bounds__(NW * 64, OCC) void dq_persist_kernel(const BwdParam
             V4 x;
 #pragma unroll
             for (int i2 = 0; i2 < 4; ++i2) x[i2] = (T)(dq[u][4 * g + i2] * p.scale);
-            *reinterpret_cast<V4*>(row + d0) = x;
+            *reinterpret_cast<TATTN_LDS V4*>(wt + Swz<D>::addr(rl, 2 * d0)) = x;
           }
         }
+      const int64_t hoff = (int64_t)(zh / p.H) * p.s[0] + (int64_t)(zh % p.H) * p.s[1];
+      T* base = (T*)p.dq + hoff + (int64_t)(qb * BMQ + 32 * w) * rs;
+      constexpr int CPRO = D / 8;  // 16-byte chunks of a row
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+#pragma unroll
+      for (int it = 0; it < 32 * CPRO / 64; ++it) {
+        const int j = ln + 64 * it;
+        const int row = j / CPRO, cc = j % CPRO;
+        const u32x4 v = *reinterpret_cast<const TATTN_LDS u32x4*>(wt + Swz<D>::addr(row, 16 * cc));
+        st16_stream(base + (int64_t)row * rs + 8 * cc, v);
+      }
     }
     if (!more) break;
     seg_of(t + 1, zh, qb);

@@ -831,7 +831,7 @@ int launch_fwd(const FwdParams& p, int D, int dtype, bool causal, int id, hipStr
 int fwd_lds_bytes(int D, int dtype, const TileEntry& e) {
   if ((dtype == 0 || dtype == 2) && e.pipe == 2) {
     const int slot = 32 * (D < 32 ? 64 : 2 * D);
-    return 2 * e.ring * slot;
+    return 2 * e.ring * slot + fwd_persist_ostage_bytes(D, e);
   }
   if (dtype == 0 || dtype == 2) {
     switch (D) {

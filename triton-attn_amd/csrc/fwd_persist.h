@@ -58,7 +58,8 @@ struct PersistLayout {
 // its O rows through its own LDS rows and stores them as whole 128-byte rows with the
 // non-temporal policy (the direct stores wrote 8-byte pieces of rows, which that policy must not
 // take: they then skip the L2's merging). Entries whose workgroups per CU would no longer fit in
-// the 160 KB of LDS keep the direct stores.
+// the 160 KB of LDS keep the direct stores, and so does head dim 128 (its 8 x 1 entry, one
+// workgroup per CU with a 64 KB stage, measured 1.3-2.7% slower non-causal from N = 2048).
 constexpr int fwd_persist_ostage_bytes(int D, const TileEntry& e) {
   const int rb = D < 32 ? 64 : 2 * D;
   const int stage = e.nw * e.tiles * 32 * rb, ring = 2 * e.ring * 32 * rb;
@@ -92,7 +93,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_persist_kernel(const FwdPara
   // -5.2%, 2048 -3.2%, 4096 -1.5%; causal N = 512 -10.9%, 1024 -5.2%, 2048 -2.5%; forward +
   // backward -1.7% / -2.8% at N = 512 (non-causal / causal), other shapes within +-0.4%.
   constexpr bool OSTAGE = fwd_persist_ostage_bytes(D, TileEntry{NW, QT, 32, OCC, 2, R}) > 0;
-  static_assert(!OSTAGE || L::RB == 128, "O staging stores rows of eight 16-byte chunks");
+  constexpr int OCPR = L::RB / 16;  // 16-byte chunks of a staged O row
+  static_assert(!OSTAGE || L::RB == 2 * D, "O staging stores whole rows without padding");
   // One array per ring slot: distinct objects let the compiler see that a DMA into one slot does
   // not alias reads of another (no conservative waits on in-flight tiles).
 #define TATTN_PSLOT(name, s) __shared__ __attribute__((aligned(256))) char name[(s) < R ? L::SLOT : 16]
@@ -552,9 +554,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void fwd_persist_kernel(const FwdPara
       int ln = lane;
       asm volatile("" : "+v"(ln));
 #pragma unroll
-      for (int it = 0; it < QT * 32 * 8 / 64; ++it) {  // 8 chunks of 16 bytes per row (D = 64)
+      for (int it = 0; it < QT * 32 * OCPR / 64; ++it) {
         const int jj = ln + 64 * it;
-        const int row = jj >> 3, cc = jj & 7;
+        const int row = jj / OCPR, cc = jj % OCPR;
         const u32x4 x = *reinterpret_cast<const TATTN_LDS u32x4*>(wt + SW::addr(row, 16 * cc));
         st16_stream(ob + (int64_t)row * p.so[2] + 8 * cc, x);
       }

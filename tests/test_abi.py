@@ -130,7 +130,8 @@ def test_bwd_noalloc_rejects_problems_past_its_workspace_before_launch():
 @pytest.mark.parametrize("dtype", [_lib.F16, _lib.BF16])
 def test_picks_at_the_benchmark_lengths(n, dtype):
     """The static picks (tattn_pick_config, batch x heads a multiple of 8) at the benchmark
-    lengths, by kind: persistent forward and dQ wherever they fit, the persistent 4-wave dK/dV at
+    lengths, by kind: persistent forward and dQ wherever they fit (forward at head dim 64: one tile
+    per wave for causal N < 2048, two otherwise), the persistent 4-wave dK/dV at
     head dim 64 for causal N < 4096 and the pipelined 8-wave one otherwise, paired-wave backward
     at 128."""
     def kind(kernel, d, causal):
@@ -139,7 +140,7 @@ def test_picks_at_the_benchmark_lengths(n, dtype):
     for causal in (False, True):
         f64, f128 = kind(_lib.K_FWD, 64, causal), kind(_lib.K_FWD, 128, causal)
         assert f64["kind"] == 2 and f64["ring"] == 4
-        assert (f64["waves"], f64["tiles"]) == ((4, 1) if causal and n < 4096 else (4, 2))
+        assert (f64["waves"], f64["tiles"]) == ((4, 1) if causal and n < 2048 else (4, 2))
         assert f128["kind"] == 2 and f128["ring"] == 4
         assert (f128["waves"], f128["tiles"]) == ((8, 1) if n >= (4096 if causal else 2048) else (4, 1))
         dkdv64, dq64 = kind(_lib.K_BWD_DKDV, 64, causal), kind(_lib.K_BWD_DQ, 64, causal)

@@ -108,10 +108,11 @@ int pick_config(int kernel, int64_t D, int dtype, int causal, int64_t N, int64_t
   switch (kernel) {
     case TATTN_K_FWD:  // persistent where it fits (D=64, 128); else 128-row blocks short, 256 / 512 long
       if (D == 64) {
-        // Persistent, ring of 4: 4 x 2 non-causal, and causal from N = 4096 (one pair of blocks per
-        // workgroup, time-sliced priority); 4 x 1 causal below. Fastest at every benchmark length
-        // (cold-cache medians, 16,384 tokens x 16 heads).
-        const int pid = causal && N < 4096 ? 5 : 7;
+        // Persistent, ring of 4: 4 x 2 non-causal, and causal from N = 2048 (from 4096 one pair of
+        // blocks per workgroup, time-sliced priority); 4 x 1 causal below. Fastest at every
+        // benchmark length (cold-cache medians, 16,384 tokens x 16 heads; causal N = 2048: 4 x 2
+        // 3% faster than 4 x 1 since both store O as whole rows, N = 1024: 4 x 1 2% faster).
+        const int pid = causal && N < 2048 ? 5 : 7;
         if (fwd_persist_fits(FwdTable<_Float16, 64>::e[pid], ZH, N, causal != 0)) return pid;
       }
       if (D == 128) {

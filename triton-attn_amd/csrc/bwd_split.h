@@ -573,24 +573,35 @@ __global__ __launch_bounds__(512, 2) void dq_split_kernel(const BwdParams p) {
   if (role_b) run(std::true_type{});
   else run(std::false_type{});
 
-  // Store (role B): the lane index is recomputed here (mbcnt) rather than kept live across the
-  // main loop.
+  // Store (role B): dQ rows (scaled, rounded) through the pair's rows of the ring, free once every
+  // wave is past its last step, then out as whole rows with the non-temporal policy (nothing in
+  // the backward reads dQ). The lane index is recomputed here (mbcnt) rather than kept live across
+  // the main loop.
+  static_assert(NP * 32 * B::RB <= B::NST * STAGE && B::RB == 2 * D, "dQ rows fit the ring");
+  __syncthreads();
   const int ln = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
-  const int qe = qw0 + (ln & 31), h2e = ln >> 5;
-  if (role_b && qe < N) {
-    T* row = (T*)p.dq + hoff + (int64_t)qe * rs;
+  const int l32e = ln & 31, h2e = ln >> 5;
+  if (role_b) {
+    TATTN_LDS char* wt = (TATTN_LDS char*)smem + pr * 32 * B::RB;
 #pragma unroll
     for (int u = 0; u < DT; ++u)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d0 = 32 * u + 8 * g + 4 * h2e;
-        if (d0 < D) {
-          V4 x;
+        V4 x;
 #pragma unroll
-          for (int i2 = 0; i2 < 4; ++i2) x[i2] = (T)(dq[u][4 * g + i2] * p.scale);
-          *reinterpret_cast<V4*>(row + d0) = x;
-        }
+        for (int i2 = 0; i2 < 4; ++i2) x[i2] = (T)(dq[u][4 * g + i2] * p.scale);
+        *reinterpret_cast<TATTN_LDS V4*>(wt + Swz<D>::addr(l32e, 2 * d0)) = x;
       }
+    constexpr int CPRO = D / 8;  // 16-byte chunks of a row
+#pragma unroll
+    for (int it = 0; it < 32 * CPRO / 64; ++it) {
+      const int j = ln + 64 * it;
+      const int row = j / CPRO, cc = j % CPRO;
+      const int qe = qw0 + row;
+      const u32x4 v = *reinterpret_cast<const TATTN_LDS u32x4*>(wt + Swz<D>::addr(row, 16 * cc));
+      if (qe < N) st16_stream((T*)p.dq + hoff + (int64_t)qe * rs + 8 * cc, v);
+    }
   }
 }
 

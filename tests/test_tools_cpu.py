@@ -207,10 +207,11 @@ def test_report_check_flags_broken_files(tmp_path):
     assert any("non-finite" in p for p in report.problems(res))
 
 
-def test_committed_suite_results_are_valid_and_rendered():
-    """results/gfx950.json (the suite's last run on an MI355X) has the current schema, every cell of
-    the grid and finite errors, and results/gfx950.md is its rendering."""
-    path = Path(__file__).resolve().parent.parent / "results" / "gfx950.json"
+@pytest.mark.parametrize("name", ["gfx950.json", "gfx950_d128.json"])
+def test_committed_suite_results_are_valid_and_rendered(name):
+    """The suite's last runs on an MI355X (head dim 64 and 128) have the current schema, every cell
+    of the grid and finite errors, and each .md next to them is its rendering."""
+    path = Path(__file__).resolve().parent.parent / "results" / name
     res = json.loads(path.read_text())
     assert report.problems(res) == []
     assert {(c["impl"], c["n"], c["mask"], c["pass"]) for c in res["cells"]} >= {
@@ -274,3 +275,37 @@ def test_each_kernel_lives_in_one_translation_unit(fwd_asm, bwd_asm, own_schedul
     assert split and all("_split_kernel" in k for k in split)
     dkdv_persist = set(re.findall(r"^\s*\.amdhsa_kernel (\S+)", dkdv_persist_asm, re.M))
     assert dkdv_persist and all("dkdv_persist_kernel" in k for k in dkdv_persist)
+
+
+@pytest.mark.skipif(not _have_hipcc(), reason="hipcc not installed")
+def test_reported_lds_matches_the_persistent_kernels(fwd_asm, own_scheduler_asm):
+    """tattn_config_desc's LDS bytes of the persistent forward and dQ entries (K/V ring, plus the
+    O rows staged at head dim 64, plus the dQ rows) agree with what the compiled kernels allocate,
+    up to the padding of the ring's unused slot arrays."""
+    from tattn import _lib
+
+    stats = {}
+    for asm in (fwd_asm, own_scheduler_asm[0], own_scheduler_asm[1]):
+        for k in diagnose.isa_stats(asm, "_kernelI").values():
+            stats[k["name"].replace("tattn::", "").split("(")[0].removeprefix("void ")] = k["lds_bytes"]
+    checked = 0
+    for d in (64, 128):
+        for cid in range(_lib.num_configs(_lib.K_FWD, d, _lib.F16)):
+            e = _lib.config_desc(_lib.K_FWD, d, _lib.F16, cid)
+            if e["kind"] != 2:
+                continue
+            for causal in ("false", "true"):
+                name = f"fwd_persist_kernel<_Float16, {d}, {e['waves']}, {e['tiles']}, 2, {causal}, {e['ring']}, false>"
+                if name not in stats:  # causal two-tile ring-8 entries run their pipelined twin
+                    continue
+                assert e["lds_bytes"] <= stats[name] <= e["lds_bytes"] + 2048, (name, e, stats[name])
+                checked += 1
+        for cid in range(_lib.num_configs(_lib.K_BWD_DQ, d, _lib.F16)):
+            e = _lib.config_desc(_lib.K_BWD_DQ, d, _lib.F16, cid)
+            if e["kind"] != 2:
+                continue
+            for causal in ("false", "true"):
+                name = f"dq_persist_kernel<_Float16, {d}, {e['waves']}, 2, {causal}>"
+                assert e["lds_bytes"] <= stats[name] <= e["lds_bytes"] + 2048, (name, e, stats[name])
+                checked += 1
+    assert checked >= 12

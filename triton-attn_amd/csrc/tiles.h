@@ -46,8 +46,9 @@ template <typename T, int D> struct FwdTable;
 // the same tiles runs it), 3 paired-wave backward, 0 generic. The 16-bit entries fit their
 // register budgets (512 / waves per SIMD) without scratch, except the non-causal persistent
 // dK/dV (28 bytes of per-lane constants, reloaded once per key block), and reach their waves per
-// SIMD within the 160 KB of LDS (a persistent forward workgroup holds a 32 KB K/V ring at D=64,
-// 64 KB at D=128). Of the fp32 kernels only causal dK/dV at D=128 spills (32 bytes).
+// SIMD within the 160 KB of LDS (a persistent forward workgroup holds a 32 KB K/V ring at D=64
+// plus 16-32 KB of O rows on their way out, a 64 KB ring at D=128). Of the fp32 kernels only
+// causal dK/dV at D=128 spills (32 bytes).
 TATTN_TABLE16(FwdTable, 16, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1})
 TATTN_TABLE16(FwdTable, 32, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 4, 1})
 TATTN_TABLE16(FwdTable, 64, {4, 2, 32, 2, 1}, {4, 1, 32, 2, 1}, {8, 1, 32, 2, 1}, {8, 2, 32, 2, 1},

@@ -422,19 +422,21 @@ def test_whole_backward_rejects_bad_dk_before_writing_anything():
     assert dq.isnan().all() and dv.isnan().all() and delta.isnan().all() and dk_buf.isnan().all()
 
 
+@pytest.mark.parametrize("heads,n", [(3, 200), (4, 512)])
 @pytest.mark.parametrize("causal", [False, True])
-def test_forward_entry_point_writes_any_output_layout(causal):
+def test_forward_entry_point_writes_any_output_layout(causal, heads, n):
     """`tattn_fwd` takes O's own strides: contiguous q, k, v with O written into a
-    [B, N, H, D] buffer viewed as [B, H, N, D] give the bits of the default layout."""
+    [B, N, H, D] buffer viewed as [B, H, N, D] give the bits of the default layout. 2 x 4 heads
+    of 512 run the persistent forward, whose O rows leave through LDS as whole rows."""
     from tattn import _lib
     from tattn.api import _forward
 
-    q, k, v = (r((2, 3, 200, 64), torch.float16, 700 + s) for s in range(3))
+    q, k, v = (r((2, heads, n, 64), torch.float16, 700 + s) for s in range(3))
     want, _ = _forward(q, k, v, causal, 0.125, save_lse=False)
-    o = torch.full((2, 200, 3, 64), float("nan"), device=DEV, dtype=torch.float16).transpose(1, 2)
+    o = torch.full((2, n, heads, 64), float("nan"), device=DEV, dtype=torch.float16).transpose(1, 2)
     st = _lib.strides4(q)
     rc = _lib.load().tattn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), None, st, st, st,
-                               _lib.strides4(o), 2, 3, 200, 64, _lib.F16, int(causal), 0.125, -1,
+                               _lib.strides4(o), 2, heads, n, 64, _lib.F16, int(causal), 0.125, -1,
                                torch.cuda.current_stream().cuda_stream)
     _lib.check(rc, "tattn_fwd")
     torch.cuda.synchronize()

@@ -360,6 +360,41 @@ def test_run_to_run_bitwise_identical(causal, dtype):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("shape", [(2, 4, 512, 64), (1, 8, 1024, 128)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("causal", [False, True])
+def test_whole_backward_in_a_token_major_layout(causal, shape):
+    """`tattn_bwd` with every tensor in one [B, N, H, D] buffer layout (the strides all tensors
+    share) gives the bits of the contiguous layout: the dQ, dK and dV rows leave the persistent and
+    paired-wave kernels as whole rows through LDS, addressed by that row stride."""
+    from tattn import _lib
+    from tattn.api import _DTYPES, _forward
+
+    z, h, n, d = shape
+    dtype = torch.float16
+    q, k, v, do = (r(shape, dtype, 900 + s) for s in range(4))
+    o, m = _forward(q, k, v, causal, 0.125)
+    lib, stream = _lib.load(), torch.cuda.current_stream().cuda_stream
+
+    def run(ts):
+        dq, dk, dv = (torch.full_like(ts[0], float("nan")) for _ in range(3))
+        delta = torch.empty((z, h, n), device=DEV, dtype=torch.float32)
+        q_, k_, v_, o_, do_ = ts
+        _lib.check(lib.tattn_bwd(q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o_.data_ptr(), do_.data_ptr(),
+                                 dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), m.data_ptr(), delta.data_ptr(),
+                                 _lib.strides4(q_), z, h, n, d, _DTYPES[dtype], int(causal), 0.125, -1, stream),
+                   "tattn_bwd")
+        torch.cuda.synchronize()
+        return dq, dk, dv
+
+    want = run([q, k, v, o, do])
+    tok = [t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v, o, do)]  # [B, N, H, D] storage
+    assert len({t.stride() for t in tok}) == 1 and tok[0].stride() != q.stride()
+    got = run(tok)
+    for name, g, w in zip(("dq", "dk", "dv"), got, want):
+        assert g.stride() == tok[0].stride()
+        assert torch.equal(g, w), name
+
+
 @pytest.mark.parametrize("shape", [(2, 3, 333, 64), (2, 4, 512, 64), (1, 8, 1024, 128)],
                          ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("dtype", DTYPES)
